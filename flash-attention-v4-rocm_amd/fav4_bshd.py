@@ -1,0 +1,113 @@
+"""Host-side binding of the gfx950 attention forward (``libfav4_bshd.so``).
+
+Mirrors the reference harness's ctypes binding, ``benchmarks/bshd.py:18-20``
+(``Args``) and ``:56-74`` (``Runner.call``): the same argument structure, the
+same argument checks, the stream taken from torch's current stream, the scale
+1/sqrt(128) by default, and a ``RuntimeError`` carrying the HIP status when the
+C ABI returns non-zero.  The library is the product; this module only moves
+pointers.  There is no fallback: if the library is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+import subprocess
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+LIB_PATH = ROOT / "build" / "libfav4_bshd.so"
+CSRC = PKG / "csrc"
+INCLUDE = ROOT / "include"
+D = 128
+
+HIPCC_FLAGS = [
+    "-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-shared",
+    f"-I{INCLUDE}", f"-I{CSRC}",
+    "-fgpu-flush-denormals-to-zero",
+    # keep the compiler from emitting packed-FP32 VALU ops (v_pk_fma_f32 & co.)
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+class Args(C.Structure):
+    """``struct Fav4Args`` (include/fav4_bshd.h): 5 pointers, 4 ints, 1 float."""
+    _fields_ = [(n, C.c_void_p) for n in ("q", "k", "v", "o", "lse")] + [
+        (n, C.c_int) for n in ("batch", "heads", "sq", "sk")] + [("scale", C.c_float)]
+
+
+def build_library(out: Path = LIB_PATH, verbose: bool = False) -> Path:
+    """Compile ``csrc/bshd.hip`` for gfx950 into ``build/libfav4_bshd.so``."""
+    out.parent.mkdir(parents=True, exist_ok=True)
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc, *HIPCC_FLAGS, str(CSRC / "bshd.hip"), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
+    if verbose and res.stderr:
+        print(res.stderr)
+    os.replace(tmp, out)
+    return out
+
+
+_LIB = None
+
+
+def load_library(path: Path = LIB_PATH) -> C.CDLL:
+    """Load the built library (raises OSError if it is missing)."""
+    global _LIB
+    if _LIB is None or Path(_LIB._name) != Path(path):
+        if not Path(path).exists():
+            raise OSError(f"{path} not built; run __graft_entry__.build() first")
+        lib = C.CDLL(str(path))
+        lib.fav4_bshd_forward.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_void_p]
+        lib.fav4_bshd_forward.restype = C.c_int
+        lib.fav4_bshd_select_config.argtypes = [C.POINTER(Args)]
+        lib.fav4_bshd_select_config.restype = C.c_int
+        _LIB = lib
+    return _LIB
+
+
+class Runner:
+    """ctypes runner with the reference harness's call signature (bshd.py:56-74)."""
+
+    def __init__(self, path: Path = LIB_PATH):
+        self.hip = load_library(path)
+
+    def args(self, q, k, v, o, lse, scale=None) -> Args:
+        import torch
+        assert all(x.dtype == torch.bfloat16 and x.is_cuda and x.is_contiguous() for x in (q, k, v, o))
+        b, sq, h, d = q.shape
+        assert d == D and k.shape == v.shape and k.shape[0] == b and tuple(k.shape[2:]) == (h, d)
+        assert o.shape == q.shape
+        assert lse is None or (tuple(lse.shape) == (b, h, sq) and lse.is_contiguous()
+                               and lse.dtype == torch.float32)
+        return Args(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                    lse.data_ptr() if lse is not None else None,
+                    b, h, sq, k.shape[1], 1 / math.sqrt(d) if scale is None else scale)
+
+    def call(self, q, k, v, o, lse, causal, config=0, scale=None, stream=None):
+        import torch
+        a = self.args(q, k, v, o, lse, scale)
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
+        status = self.hip.fav4_bshd_forward(C.byref(a), int(causal), int(config), stream)
+        if status:
+            raise RuntimeError(f"config {config}: HIP status {status}")
+
+    def select_config(self, q, k) -> int:
+        b, sq, h, _ = q.shape
+        a = Args(None, None, None, None, None, b, h, sq, k.shape[1], 1 / math.sqrt(D))
+        return self.hip.fav4_bshd_select_config(C.byref(a))
+
+
+def forward(q, k, v, causal=False, with_lse=False, config=0, scale=None):
+    """Allocate O (and LSE) and run the forward; returns (o, lse or None)."""
+    import torch
+    o = torch.empty_like(q)
+    lse = (torch.empty((q.shape[0], q.shape[2], q.shape[1]), device=q.device, dtype=torch.float32)
+           if with_lse else None)
+    Runner().call(q, k, v, o, lse, causal, config, scale)
+    return o, lse

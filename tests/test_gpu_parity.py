@@ -1,0 +1,88 @@
+"""GPU parity of fav4_bshd_forward (through the C ABI) against the FP64 oracle.
+
+Mirrors the reference validation, benchmarks/bshd.py:103-129: outputs are
+prefilled with NaN so an unwritten element fails, every case runs dense and
+causal, every config ID, with and without LSE.  Two bars are asserted:
+
+* the reference harness's BF16 tolerance (bshd.py:25,30-31): elementwise
+  |o - ref| <= 0.01 + 0.01|ref|, RMS-relative <= 0.005, LSE max-abs <= 2e-4,
+  all outputs finite -- on the reference's own ten validation cases;
+* the port's acceptance bar: O max-abs <= 2e-2, LSE max-abs <= 1e-3, finite --
+  on every case, including the large-logit ragged stress shape.
+"""
+import numpy as np
+import pytest
+
+from oracle import attention as orc
+from tests.conftest import to_device, to_host_bits
+
+pytestmark = pytest.mark.gpu
+
+CONFIGS = (0, 1, 2, 3)
+
+
+def _run_all(runner, q, k, v, causal, ref, ref_lse, configs=CONFIGS, rows=None, bar="reference"):
+    import torch
+    dev = torch.device("cuda:0")
+    qd, kd, vd = to_device(q, dev), to_device(k, dev), to_device(v, dev)
+    b, sq, h, _ = q.shape
+    o = torch.empty_like(qd)
+    lse = torch.empty((b, h, sq), device=dev, dtype=torch.float32)
+    results = []
+    for config in configs:
+        for with_lse in (False, True):
+            o.fill_(float("nan"))
+            lse.fill_(float("nan"))
+            print(f"  config={config} lse={with_lse}", flush=True)
+            runner.call(qd, kd, vd, o, lse if with_lse else None, causal, config)
+            torch.cuda.synchronize()
+            got = to_host_bits(o)
+            got_lse = lse.cpu().numpy() if with_lse else None
+            if rows is not None:
+                got = got[:, rows]
+                got_lse = got_lse[:, :, rows] if with_lse else None
+            e = orc.errors(got, got_lse, ref, ref_lse if with_lse else None)
+            ok = orc.check_north_star_tolerance(e)
+            if bar == "reference":
+                ok = ok and orc.check_reference_tolerance(e)
+            results.append((config, with_lse, ok, e))
+            if not with_lse:
+                # LSE = NULL must leave the LSE buffer untouched
+                assert torch.isnan(lse).all().item(), f"config {config} wrote LSE with lse=NULL"
+    return results
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
+@pytest.mark.parametrize("case", orc.VALIDATION_CASES, ids=lambda c: f"b{c[0]}h{c[1]}_{c[2]}x{c[3]}_{c[4]}")
+def test_reference_validation_cases(gpu_runner, case, causal):
+    b, h, sq, sk, pattern = case
+    print(f"case {case} causal={causal}", flush=True)
+    q, k, v = orc.make_inputs(b, h, sq, sk, pattern)
+    ref, ref_lse = orc.attention_fp64(q, k, v, orc.DEFAULT_SCALE, causal)
+    res = _run_all(gpu_runner, q, k, v, causal, ref, ref_lse)
+    bad = [(c, l, e) for c, l, ok, e in res if not ok]
+    assert not bad, f"{len(bad)}/{len(res)} failed: {bad[:3]}"
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
+def test_validation_scale_b2h4s256(gpu_runner, causal):
+    """Validation-scale shape: B2 H4 Sq=Sk=256, N(0,1), scale 1/sqrt(128), LSE on."""
+    q, k, v = orc.make_inputs(2, 4, 256, 256, "normal")
+    ref, ref_lse = orc.attention_fp64(q, k, v, orc.DEFAULT_SCALE, causal)
+    res = _run_all(gpu_runner, q, k, v, causal, ref, ref_lse)
+    bad = [(c, l, e) for c, l, ok, e in res if not ok]
+    assert not bad, bad[:3]
+
+
+def test_ragged_stress_b4h16_1000x3077(gpu_runner):
+    """Ragged tails + large logits: B4 H16 Sq1000 Sk3077, top-left causal, LSE on,
+    10 % of Q rows x16 and 1 % of K rows x64 (forces conditional rescales)."""
+    q, k, v = orc.make_inputs(4, 16, 1000, 3077, "stress")
+    for causal in (True, False):
+        print(f"stress causal={causal}", flush=True)
+        ref, ref_lse = orc.attention_fp64(q, k, v, orc.DEFAULT_SCALE, causal)
+        res = _run_all(gpu_runner, q, k, v, causal, ref, ref_lse, bar="north_star")
+        for c, l, ok, e in res:
+            print(f"    config={c} lse={l} ok={ok} {e}")
+        bad = [(c, l, e) for c, l, ok, e in res if not ok]
+        assert not bad, bad[:3]
