@@ -53,7 +53,29 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     p.add_argument("--sweep", default="", help="comma list of extra sequence lengths to time (report only)")
+    p.add_argument("--pmc-pass", action="store_true",
+                   help="profiling mode for counter runs: two eager launches per mask type, then a "
+                        "plain 1 GiB device copy (HBM counter calibration); prints no JSON")
     return p.parse_args()
+
+
+def pmc_pass(torch, runner, args):
+    """Eager launches for rocprofv3 --pmc runs (no graphs, one dispatch per launch)."""
+    b, h, s = args.batch, args.heads, args.seq
+    q, k, v = make_inputs(torch, b, h, s)
+    o = torch.empty_like(q)
+    for causal in (False, True):
+        for _ in range(2):
+            runner.call(q, k, v, o, None, causal, args.config)
+        torch.cuda.synchronize()
+        print(f"# pmc-pass launched B{b} H{h} S{s} causal={causal} x2", flush=True)
+    del q, k, v, o
+    src = torch.ones(1 << 28, device="cuda", dtype=torch.float32)    # 1 GiB
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("# pmc-pass copy: 1073741824 bytes read + 1073741824 bytes written per dispatch", flush=True)
 
 
 def make_inputs(torch, b, h, s, seed=11939):
@@ -156,6 +178,9 @@ def main():
     import __graft_entry__
     pkg = __graft_entry__.import_package()
     runner = pkg.Runner()
+    if args.pmc_pass:
+        pmc_pass(torch, runner, args)
+        return
 
     b, h, s = args.batch, args.heads, args.seq
     q, k, v = make_inputs(torch, b, h, s)
