@@ -43,21 +43,29 @@ constexpr float RESCALE_THRESHOLD = 8.f;         // log2 units (src/bshd_kernel.
 __device__ __forceinline__ int k_swz(int r) { return r & 15; }
 __device__ __forceinline__ int v_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
-// Work item -> (bh, q tile).  Dense: the hardware deals workgroups round-robin
-// over the 8 XCDs, so remap ids to give each XCD a contiguous run of items and
-// keep one head's K/V hot in that XCD's L2.  Causal: heaviest q tiles first.
+// Work items.  The hardware deals workgroups round-robin over the 8 XCDs, so
+// item ids are remapped to give each XCD a contiguous run of items: all q
+// tiles of one (batch, head) then run at the same time on one XCD and share
+// its L2 copy of that head's K/V.  Dense: one item = one q tile.  Causal: one
+// item = the pair of q tiles (j, tiles-1-j), heavy one first, so every item
+// costs tiles+1 key tiles and the grid has no tail of light items.
 template <bool CAUSAL>
-__device__ __forceinline__ void map_work(int id, int tiles, int bh_count, int& bh, int& tile) {
-    if constexpr (CAUSAL) {
-        tile = tiles - 1 - id / bh_count;
-        bh = id - (id / bh_count) * bh_count;
-    } else {
-        const int total = tiles * bh_count;
-        const int xcd = id & 7, slot = id >> 3;
-        const int per = total >> 3, rem = total & 7;
+__host__ __device__ constexpr int items_per_head(int tiles) { return CAUSAL ? (tiles + 1) / 2 : tiles; }
+
+template <bool CAUSAL, class F>
+__device__ __forceinline__ void for_each_item(int tiles, int total, F&& process) {
+    const int per_head = items_per_head<CAUSAL>(tiles);
+    for (int id = blockIdx.x; id < total; id += gridDim.x) {
+        const int xcd = id & 7, slot = id >> 3, per = total >> 3, rem = total & 7;
         const int logical = xcd * per + min(xcd, rem) + slot;
-        bh = logical / tiles;
-        tile = logical - bh * tiles;
+        const int bh = __builtin_amdgcn_readfirstlane(logical / per_head);
+        const int j = __builtin_amdgcn_readfirstlane(logical - bh * per_head);
+        if constexpr (CAUSAL) {
+            const int n = (j == tiles - 1 - j) ? 1 : 2;
+            for (int k = 0; k < n; ++k) process(bh, k == 0 ? tiles - 1 - j : j);
+        } else {
+            process(bh, j);
+        }
     }
 }
 
@@ -75,26 +83,24 @@ struct LdsOffsets {
     uint32_t v[2][4];   // V^T operand: [first/second 4-key group][32-dim block]
 };
 
-// One key tile: S^T = K.Q^T, online softmax, O^T += V^T.P^T.
-// MASKED selects the diagonal / tail variant.
-template <int BN, bool MASKED, bool CAUSAL, bool LSE>
-__device__ __forceinline__ void attend_tile(const unsigned char* ks, const unsigned char* vs,
-                                            const LdsOffsets& off, const bf16x8 (&qr)[8], RowState& st,
-                                            bool first, int start, int sk, int qw, int row, int half,
-                                            float scale2) {
+// A 32-key block of tile `start` is visible to the wave holding rows
+// [qw, qw+32) unless it lies past the key length or entirely above the
+// causal diagonal.
+template <bool MASKED, bool CAUSAL>
+__device__ __forceinline__ bool block_active(int k0, int sk, int qw) {
+    return !MASKED || (k0 < sk && (!CAUSAL || k0 <= qw + 31));
+}
+
+// S^T = K.Q^T for one tile: 8 MFMAs per 32-key block, K operands read ahead.
+template <int BN, bool MASKED, bool CAUSAL>
+__device__ __forceinline__ void tile_qk(const unsigned char* ks, const LdsOffsets& off, const bf16x8 (&qr)[8],
+                                        f32x16 (&s)[BN / 32], int start, int sk, int qw) {
     constexpr int KB = BN / 32;
     const f32x16 zero = {};
-    bool active[KB];
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-        active[kb] = !MASKED || (start + kb * 32 < sk && (!CAUSAL || start + kb * 32 <= qw + 31));
-
-    // ---- S^T = K . Q^T (8 MFMAs per 32-key block, K operands prefetched) ----
-    f32x16 s[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
         s[kb] = zero;
-        if (!MASKED || active[kb]) {
+        if (block_active<MASKED, CAUSAL>(start + kb * 32, sk, qw)) {
             bf16x8 kop[8];
 #pragma unroll
             for (int c = 0; c < 8; ++c) kop[c] = lds_read16(ks + kb * 32 * ROW_BYTES + off.k[c]);
@@ -103,13 +109,25 @@ __device__ __forceinline__ void attend_tile(const unsigned char* ks, const unsig
             for (int c = 1; c < 8; ++c) s[kb] = mfma32(kop[c], qr[c], s[kb]);
         }
     }
+}
 
-    // ---- masks (key index of element v of lane (col, half) in block kb) ----
+// Softmax values carried from the head to the tail of one tile.
+struct SmCarry {
+    float alpha;      // exp2(m_old - m_new) per lane (1 when the base did not move)
+    float neg;        // -m_new
+    float pb0, pb1;   // partial sums of the BF16 weights
+    float part[4];    // partial FP32 sums (LSE only)
+    bool rescale;     // some lane of the wave moved its base: O must be rescaled
+};
+
+// Masks of one tile (diagonal / tail variant only).
+template <int BN, bool MASKED, bool CAUSAL>
+__device__ __forceinline__ void tile_mask(f32x16 (&s)[BN / 32], int start, int sk, int qw, int row, int half) {
     if constexpr (MASKED) {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
+        for (int kb = 0; kb < BN / 32; ++kb) {
             const int k0 = start + kb * 32;
-            if (!active[kb]) {
+            if (!block_active<MASKED, CAUSAL>(k0, sk, qw)) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) s[kb][v] = -__builtin_inff();
             } else if (k0 + 32 > sk || (CAUSAL && k0 + 31 > qw)) {
@@ -122,8 +140,41 @@ __device__ __forceinline__ void attend_tile(const unsigned char* ks, const unsig
             }
         }
     }
+}
 
-    // ---- online softmax with the conditional rescale (log2 units) ----
+// P = exp2(s*scale2 - m) for one 32-key block, as two BF16 MFMA B operands.
+template <bool LSE>
+__device__ __forceinline__ void exp_block(const f32x16& s, bf16x8 (&p)[2], SmCarry& c, float scale2) {
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+        f32x2 e[4];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float x = exp2_native(fmaf(s[sub * 8 + i], scale2, c.neg));
+            e[i >> 1][i & 1] = x;
+            if constexpr (LSE) c.part[i & 3] += x;
+        }
+        const bf16x2 b0 = __builtin_convertvector(e[0], bf16x2);
+        const bf16x2 b1 = __builtin_convertvector(e[1], bf16x2);
+        const bf16x2 b2 = __builtin_convertvector(e[2], bf16x2);
+        const bf16x2 b3 = __builtin_convertvector(e[3], bf16x2);
+        c.pb0 = bf16_pair_sum(b0, c.pb0);
+        c.pb1 = bf16_pair_sum(b1, c.pb1);
+        c.pb0 = bf16_pair_sum(b2, c.pb0);
+        c.pb1 = bf16_pair_sum(b3, c.pb1);
+        p[sub] = bf16x8{b0[0], b0[1], b1[0], b1[1], b2[0], b2[1], b3[0], b3[1]};
+    }
+}
+
+// Softmax head: masks, row max, conditional base update (log2 units), P of
+// the first 32-key block.  The O rescale it decides is applied by
+// apply_rescale before the tile's PV product.
+template <int BN, bool MASKED, bool CAUSAL, bool LSE>
+__device__ __forceinline__ void softmax_head(f32x16 (&s)[BN / 32], bf16x8 (&p)[BN / 32][2], RowState& st,
+                                             SmCarry& c, bool first, int start, int sk, int qw, int row,
+                                             int half, float scale2) {
+    constexpr int KB = BN / 32;
+    tile_mask<BN, MASKED, CAUSAL>(s, start, sk, qw, row, half);
     float mx = -__builtin_inff();
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
@@ -133,45 +184,53 @@ __device__ __forceinline__ void attend_tile(const unsigned char* ks, const unsig
     const float cand = fmaxf(st.m, mx * scale2);
     const bool update = first || cand > st.m + RESCALE_THRESHOLD;
     const float next = update ? cand : st.m;
-    const float alpha = exp2_native(st.m - next);   // 0 on the first tile, 1 if no update
-    if (!first && __builtin_amdgcn_ballot_w64(update)) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db) st.o[db] *= alpha;
-    }
+    c.alpha = exp2_native(st.m - next);   // 0 on the first tile, 1 if no update
+    c.rescale = !first && __builtin_amdgcn_ballot_w64(update) != 0;
     st.m = next;
-    const float neg = -next;
-    float part[4] = {0.f, 0.f, 0.f, 0.f};
-    float pb0 = 0.f, pb1 = 0.f;
-    bf16x8 p[KB][2];
+    c.neg = -next;
+    c.pb0 = c.pb1 = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            f32x2 e[4];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float x = exp2_native(fmaf(s[kb][sub * 8 + i], scale2, neg));
-                e[i >> 1][i & 1] = x;
-                if constexpr (LSE) part[i & 3] += x;
-            }
-            const bf16x2 b0 = __builtin_convertvector(e[0], bf16x2);
-            const bf16x2 b1 = __builtin_convertvector(e[1], bf16x2);
-            const bf16x2 b2 = __builtin_convertvector(e[2], bf16x2);
-            const bf16x2 b3 = __builtin_convertvector(e[3], bf16x2);
-            pb0 = bf16_pair_sum(b0, pb0);
-            pb1 = bf16_pair_sum(b1, pb1);
-            pb0 = bf16_pair_sum(b2, pb0);
-            pb1 = bf16_pair_sum(b3, pb1);
-            p[kb][sub] = bf16x8{b0[0], b0[1], b1[0], b1[1], b2[0], b2[1], b3[0], b3[1]};
-        }
-    }
-    st.lb = st.lb * alpha + xhalf_sum(pb0 + pb1);
-    if constexpr (LSE) st.l = st.l * alpha + xhalf_sum((part[0] + part[1]) + (part[2] + part[3]));
+    for (int i = 0; i < 4; ++i) c.part[i] = 0.f;
+    exp_block<LSE>(s[0], p[0], c, scale2);
+}
 
-    // ---- O^T += V^T . P^T  (S element v of lane half h is MFMA k = h*8 + v%8) ----
+// Softmax tail: P of the remaining blocks, running sums.
+template <int BN, bool LSE>
+__device__ __forceinline__ void softmax_tail(const f32x16 (&s)[BN / 32], bf16x8 (&p)[BN / 32][2], RowState& st,
+                                             SmCarry& c, float scale2) {
+#pragma unroll
+    for (int kb = 1; kb < BN / 32; ++kb) exp_block<LSE>(s[kb], p[kb], c, scale2);
+    st.lb = st.lb * c.alpha + xhalf_sum(c.pb0 + c.pb1);
+    if constexpr (LSE) st.l = st.l * c.alpha + xhalf_sum((c.part[0] + c.part[1]) + (c.part[2] + c.part[3]));
+}
+
+__device__ __forceinline__ void apply_rescale(RowState& st, const SmCarry& c) {
+    if (c.rescale) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) st.o[db] *= c.alpha;
+    }
+}
+
+// Whole-tile softmax (single-group kernel).
+template <int BN, bool MASKED, bool CAUSAL, bool LSE>
+__device__ __forceinline__ void tile_softmax(f32x16 (&s)[BN / 32], bf16x8 (&p)[BN / 32][2], RowState& st,
+                                             bool first, int start, int sk, int qw, int row, int half,
+                                             float scale2) {
+    SmCarry c;
+    softmax_head<BN, MASKED, CAUSAL, LSE>(s, p, st, c, first, start, sk, qw, row, half, scale2);
+    apply_rescale(st, c);
+    softmax_tail<BN, LSE>(s, p, st, c, scale2);
+}
+
+// O^T += V^T.P^T for one tile (S element v of lane half h is MFMA k = h*8 + v%8).
+template <int BN, bool MASKED, bool CAUSAL>
+__device__ __forceinline__ void tile_pv(const unsigned char* vs, const LdsOffsets& off,
+                                        const bf16x8 (&p)[BN / 32][2], RowState& st, int start, int sk,
+                                        int qw) {
+    constexpr int KB = BN / 32;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-        if (MASKED && !active[kb]) continue;
+        if (!block_active<MASKED, CAUSAL>(start + kb * 32, sk, qw)) continue;
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             const unsigned char* vb = vs + (kb * 32 + sub * 16) * ROW_BYTES;
@@ -188,17 +247,29 @@ __device__ __forceinline__ void attend_tile(const unsigned char* ks, const unsig
     }
 }
 
-template <int WAVES, int BN, bool CAUSAL, bool LSE>
+// WAVES waves x 32 query rows per workgroup, BN keys per tile, STAGES LDS
+// buffers of K+V.  PINGPONG (8 waves, 3 stages): waves 0-3 run QK(t),
+// softmax(t), PV(t) between barriers t and t+1 while waves 4-7 (one of each
+// group per SIMD) run softmax(t-1), PV(t-1), QK(t), so one wave's softmax
+// VALU work overlaps the other wave's MFMAs on the same SIMD.  Tile t lives
+// in stage t % STAGES; the DMA of tile t+1 is issued right after barrier t
+// into the stage that tile t-2 used (read before barrier t by everyone).
+template <int WAVES, int BN, bool CAUSAL, bool LSE, int STAGES, bool PINGPONG>
 __global__ __launch_bounds__(WAVES * 64)
 void fwd_kernel(Fav4Args a, int tiles, int total) {
     constexpr int BM = WAVES * 32;
+    constexpr int KB = BN / 32;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
+    constexpr int STAGE_BYTES = 2 * TILE_BYTES;          // K then V
     constexpr int DMA = BN / 4 / WAVES;                  // 1 KiB DMA ops per wave per matrix
     static_assert(BN % 32 == 0 && BN % (4 * WAVES) == 0, "tile shape");
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TILE_BYTES];  // K0 V0 K1 V1
+    static_assert(!PINGPONG || (WAVES == 8 && STAGES == 3), "ping-pong needs two 4-wave groups, 3 stages");
+    static_assert(STAGES == 2 || STAGES == 3, "stages");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[STAGES * STAGE_BYTES];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool lagging = PINGPONG && wave >= 4;           // group that runs half a tile behind
     const int col = lane & 31, half = lane >> 5;
     const uint32_t row_bytes = uint32_t(a.heads) * ROW_BYTES;   // stride between sequence positions
     const float scale2 = a.scale * LOG2E;
@@ -227,11 +298,7 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
         dv[i] = r * row_bytes + ((p ^ v_swz(r)) << 4);
     }
 
-    for (int id = blockIdx.x; id < total; id += gridDim.x) {
-        int bh, tile;
-        map_work<CAUSAL>(id, tiles, a.batch * a.heads, bh, tile);
-        bh = __builtin_amdgcn_readfirstlane(bh);
-        tile = __builtin_amdgcn_readfirstlane(tile);
+    auto process = [&](int bh, int tile) {
         const int batch = bh / a.heads, head = bh - batch * a.heads;
         const int q0 = tile * BM, qw = q0 + wave * 32;
         const int row = qw + col;                                 // this lane's query row
@@ -254,7 +321,7 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
             const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * row_bytes + ROW_BYTES;
             const u32x4 rk = make_desc(kbase + first * row_bytes, bytes);
             const u32x4 rv = make_desc(vbase + first * row_bytes, bytes);
-            const uint32_t ks = smem_base + stage * 2 * TILE_BYTES + wave * DMA * 1024;
+            const uint32_t ks = smem_base + stage * STAGE_BYTES + wave * DMA * 1024;
 #pragma unroll
             for (int i = 0; i < DMA; ++i) {
                 dma16(rk, ks + i * 1024, dk[i]);
@@ -279,36 +346,75 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
         st.m = -__builtin_inff();
         st.lb = 0.f;
         st.l = 0.f;
+        f32x16 s[KB];
+        bf16x8 p[KB][2];
 
-        // One pipeline step on a compile-time stage: wait for tile t, prefetch
-        // tile t+1 into the other stage, then attend to tile t.
-        auto step = [&](auto stage_c, auto masked_c, int t) {
+        // One pipeline step on compile-time stages: wait for tile t, prefetch
+        // tile t+1, then this wave's share of the work between two barriers.
+        // LAG selects the lagging group's order (softmax+PV of t-1, then QK of t).
+        auto step = [&](auto lag_c, auto stage_c, auto mprev_c, auto mcur_c, int t) {
+            constexpr bool LAG = decltype(lag_c)::value;
             constexpr int STAGE = decltype(stage_c)::value;
-            constexpr bool MASKED = decltype(masked_c)::value;
+            constexpr int PREV = (STAGE + STAGES - 1) % STAGES;
+            constexpr bool MPREV = decltype(mprev_c)::value, MCUR = decltype(mcur_c)::value;
+            const unsigned char* cur = smem + STAGE * STAGE_BYTES;
+            const unsigned char* prv = smem + PREV * STAGE_BYTES;
             wait_vmem();        // this wave's DMA of tile t has landed
-            __syncthreads();    // ... and every other wave's; the other stage is free
-            if (t + 1 < ntiles) issue(t + 1, STAGE ^ 1);
-            attend_tile<BN, MASKED, CAUSAL, LSE>(smem + STAGE * 2 * TILE_BYTES,
-                                                 smem + STAGE * 2 * TILE_BYTES + TILE_BYTES, off, qr, st,
-                                                 t == 0, t * BN, a.sk, qw, row, half, scale2);
+            __syncthreads();    // ... and every other wave's; stage (t+1)%STAGES is free
+            if (t + 1 < ntiles) issue(t + 1, (STAGE + 1) % STAGES);
+            if constexpr (!LAG) {
+                tile_qk<BN, MCUR, CAUSAL>(cur, off, qr, s, t * BN, a.sk, qw);
+                tile_softmax<BN, MCUR, CAUSAL, LSE>(s, p, st, t == 0, t * BN, a.sk, qw, row, half, scale2);
+                tile_pv<BN, MCUR, CAUSAL>(cur + TILE_BYTES, off, p, st, t * BN, a.sk, qw);
+            } else {
+                if (t > 0) {
+                    tile_softmax<BN, MPREV, CAUSAL, LSE>(s, p, st, t == 1, (t - 1) * BN, a.sk, qw, row, half,
+                                                         scale2);
+                    tile_pv<BN, MPREV, CAUSAL>(prv + TILE_BYTES, off, p, st, (t - 1) * BN, a.sk, qw);
+                }
+                tile_qk<BN, MCUR, CAUSAL>(cur, off, qr, s, t * BN, a.sk, qw);
+            }
         };
         using S0 = std::integral_constant<int, 0>;
         using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
         using Plain = std::integral_constant<bool, false>;
         using Masked = std::integral_constant<bool, true>;
-        int t = 0;
-        for (; t + 1 < nfull; t += 2) {
-            step(S0{}, Plain{}, t);
-            step(S1{}, Plain{}, t + 1);
-        }
-        if (t < nfull) {
-            step(S0{}, Plain{}, t);
-            ++t;
-        }
-        for (; t < ntiles; ++t) {
-            if (t & 1) step(S1{}, Masked{}, t);
-            else step(S0{}, Masked{}, t);
-        }
+        // The whole key loop of one group (both groups run the same barriers).
+        auto key_loop = [&](auto lag_c) {
+            int t = 0;
+            if constexpr (STAGES == 2) {
+                for (; t + 1 < nfull; t += 2) {
+                    step(lag_c, S0{}, Plain{}, Plain{}, t);
+                    step(lag_c, S1{}, Plain{}, Plain{}, t + 1);
+                }
+                for (; t < ntiles; ++t) {
+                    if (t & 1) step(lag_c, S1{}, Masked{}, Masked{}, t);
+                    else step(lag_c, S0{}, Masked{}, Masked{}, t);
+                }
+            } else {
+                for (; t + 2 < nfull; t += 3) {
+                    step(lag_c, S0{}, Plain{}, Plain{}, t);
+                    step(lag_c, S1{}, Plain{}, Plain{}, t + 1);
+                    step(lag_c, S2{}, Plain{}, Plain{}, t + 2);
+                }
+                for (; t < ntiles; ++t) {
+                    const int r = t % 3;
+                    if (r == 0) step(lag_c, S0{}, Masked{}, Masked{}, t);
+                    else if (r == 1) step(lag_c, S1{}, Masked{}, Masked{}, t);
+                    else step(lag_c, S2{}, Masked{}, Masked{}, t);
+                }
+            }
+            if constexpr (decltype(lag_c)::value) {
+                // The lagging group still owes softmax + PV of the last tile.
+                const int tl = ntiles - 1;
+                const unsigned char* vlast = smem + (tl % STAGES) * STAGE_BYTES + TILE_BYTES;
+                tile_softmax<BN, true, CAUSAL, LSE>(s, p, st, tl == 0, tl * BN, a.sk, qw, row, half, scale2);
+                tile_pv<BN, true, CAUSAL>(vlast, off, p, st, tl * BN, a.sk, qw);
+            }
+        };
+        if (PINGPONG && lagging) key_loop(std::integral_constant<bool, PINGPONG>{});
+        else key_loop(std::integral_constant<bool, false>{});
 
         // Epilogue: O = acc / lb in BF16; rows >= sq fall outside the store bound.
         // Dividing by the sum of the rounded weights keeps them normalised, so
@@ -331,7 +437,253 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
             if (half == 0 && row < a.sq) a.lse[int64_t(bh) * a.sq + row] = st.m * LN2 + logf(st.l);
         }
         __syncthreads();   // LDS stages are reused by the next work item
+    };
+    for_each_item<CAUSAL>(tiles, total, process);
+}
+
+// ---------------------------------------------------------------------------
+// Two-group kernel: 4 waves x 64 query rows, one wave per SIMD (512 registers).
+// Each wave holds two 32-row groups, A = rows [qa, qa+32) and B = [qa+32,
+// qa+64), that share every K and V operand read from LDS (half the LDS
+// traffic per FLOP of the one-group kernel).  The key loop is software
+// pipelined so that one group's softmax VALU work sits beside the other
+// group's MFMAs in the same instruction stream:
+//   P1: load K(t); QK_A(t)            | softmax tail  B(t-1)
+//   P2: PV_B(t-1) (V(t-1) registers)  | softmax head  A(t)
+//   P3: QK_B(t) (K(t) registers)      | softmax tail  A(t)
+//   P4: load V(t); PV_A(t)            | softmax head  B(t)
+// Only tile t's LDS stage is read between barriers t and t+1, so two stages
+// suffice; the DMA of tile t+1 is issued right after barrier t.
+// ---------------------------------------------------------------------------
+template <int BN, bool MASKED, bool CAUSAL>
+__device__ __forceinline__ void load_k(const unsigned char* ks, const LdsOffsets& off, bf16x8 (&kr)[BN / 32][8],
+                                       int start, int sk, int qlast) {
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb)
+        if (block_active<MASKED, CAUSAL>(start + kb * 32, sk, qlast)) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) kr[kb][c] = lds_read16(ks + kb * 32 * ROW_BYTES + off.k[c]);
+        }
+}
+
+template <int BN, bool MASKED, bool CAUSAL>
+__device__ __forceinline__ void qk_regs(const bf16x8 (&kr)[BN / 32][8], const bf16x8 (&qr)[8], f32x16 (&s)[BN / 32],
+                                        int start, int sk, int qw) {
+    const f32x16 zero = {};
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb) {
+        s[kb] = zero;
+        if (block_active<MASKED, CAUSAL>(start + kb * 32, sk, qw)) {
+            s[kb] = mfma32(kr[kb][0], qr[0], zero);
+#pragma unroll
+            for (int c = 1; c < 8; ++c) s[kb] = mfma32(kr[kb][c], qr[c], s[kb]);
+        }
     }
+}
+
+template <int BN, bool MASKED, bool CAUSAL>
+__device__ __forceinline__ void load_v(const unsigned char* vs, const LdsOffsets& off, bf16x8 (&vr)[BN / 32][2][4],
+                                       int start, int sk, int qlast) {
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb)
+        if (block_active<MASKED, CAUSAL>(start + kb * 32, sk, qlast)) {
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+                const unsigned char* vb = vs + (kb * 32 + sub * 16) * ROW_BYTES;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const bf16x4 lo = lds_read_tr(vb + off.v[0][db]);
+                    const bf16x4 hi = lds_read_tr(vb + off.v[1][db]);
+                    vr[kb][sub][db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+            }
+        }
+}
+
+template <int BN, bool MASKED, bool CAUSAL>
+__device__ __forceinline__ void pv_regs(const bf16x8 (&vr)[BN / 32][2][4], const bf16x8 (&p)[BN / 32][2],
+                                        RowState& st, int start, int sk, int qw) {
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb)
+        if (block_active<MASKED, CAUSAL>(start + kb * 32, sk, qw)) {
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for (int db = 0; db < 4; ++db) st.o[db] = mfma32(vr[kb][sub][db], p[kb][sub], st.o[db]);
+        }
+}
+
+template <int BN, bool CAUSAL, bool LSE>
+__global__ __launch_bounds__(256)
+void fwd_kernel_g2(Fav4Args a, int tiles, int total) {
+    constexpr int WAVES = 4, BM = 256;
+    constexpr int KB = BN / 32;
+    constexpr int TILE_BYTES = BN * ROW_BYTES;
+    constexpr int STAGE_BYTES = 2 * TILE_BYTES;          // K then V
+    constexpr int DMA = BN / 4 / WAVES;                  // 1 KiB DMA ops per wave per matrix
+    static_assert(BN % 32 == 0 && BN % (4 * WAVES) == 0, "tile shape");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 31, half = lane >> 5;
+    const uint32_t row_bytes = uint32_t(a.heads) * ROW_BYTES;
+    const float scale2 = a.scale * LOG2E;
+    const uint32_t smem_base = lds_addr(smem);
+
+    LdsOffsets off;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) off.k[c] = col * ROW_BYTES + ((((2 * c) | half) ^ k_swz(col)) << 4);
+    {
+        const int r0 = half * 4 + ((lane & 15) >> 2);
+        const int gl = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r = r0 + 8 * j;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+                off.v[j][db] = r * ROW_BYTES + (((db * 4 + gl) ^ v_swz(r)) << 4) + ((lane & 1) << 3);
+        }
+    }
+    uint32_t dk[DMA], dv[DMA];
+#pragma unroll
+    for (int i = 0; i < DMA; ++i) {
+        const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
+        dk[i] = r * row_bytes + ((p ^ k_swz(r)) << 4);
+        dv[i] = r * row_bytes + ((p ^ v_swz(r)) << 4);
+    }
+
+    auto process = [&](int bh, int tile) {
+        const int batch = bh / a.heads, head = bh - batch * a.heads;
+        const int q0 = tile * BM, qa = q0 + wave * 64, qb = qa + 32;
+        const int row_a = qa + col, row_b = qb + col;
+        const int64_t qrow0 = (int64_t(batch) * a.sq + q0) * a.heads + head;
+        const int64_t krow0 = int64_t(batch) * a.sk * a.heads + head;
+        const char* kbase = static_cast<const char*>(a.k) + krow0 * ROW_BYTES;
+        const char* vbase = static_cast<const char*>(a.v) + krow0 * ROW_BYTES;
+        const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + qrow0 * ROW_BYTES,
+                                    uint32_t(a.sq - q0 - 1) * row_bytes + ROW_BYTES);
+        const rsrc_t ro = make_rsrc(static_cast<char*>(a.o) + qrow0 * ROW_BYTES,
+                                    uint32_t(a.sq - q0 - 1) * row_bytes + ROW_BYTES);
+        const int kend = CAUSAL ? min(a.sk, q0 + BM) : a.sk;
+        const int ntiles = (kend + BN - 1) / BN;
+        const int nfull = (CAUSAL ? min(a.sk, q0 + 1) : a.sk) / BN;
+
+        auto issue = [&](int t, int stage) {
+            const int64_t first = int64_t(t) * BN;
+            const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * row_bytes + ROW_BYTES;
+            const u32x4 rk = make_desc(kbase + first * row_bytes, bytes);
+            const u32x4 rv = make_desc(vbase + first * row_bytes, bytes);
+            const uint32_t ks = smem_base + stage * STAGE_BYTES + wave * DMA * 1024;
+#pragma unroll
+            for (int i = 0; i < DMA; ++i) {
+                dma16(rk, ks + i * 1024, dk[i]);
+                dma16(rv, ks + TILE_BYTES + i * 1024, dv[i]);
+            }
+        };
+
+        issue(0, 0);
+        bf16x8 qra[8], qrb[8];
+        {
+            const uint32_t qoff = uint32_t(wave * 64 + col) * row_bytes + half * 16;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                qra[c] = load16(rq, qoff + c * 32);
+                qrb[c] = load16(rq, qoff + 32 * row_bytes + c * 32);
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) asm volatile("" ::"v"(qra[c]), "v"(qrb[c]));
+        }
+        RowState sa, sb;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) sa.o[db] = sb.o[db] = f32x16{};
+        sa.m = sb.m = -__builtin_inff();
+        sa.lb = sb.lb = 0.f;
+        sa.l = sb.l = 0.f;
+        f32x16 s_a[KB], s_b[KB];
+        bf16x8 p_a[KB][2], p_b[KB][2];
+        bf16x8 kr[KB][8], vr[KB][2][4];
+        SmCarry ca, cb;
+
+        auto iter = [&](auto stage_c, auto masked_c, auto first_c, int t) {
+            constexpr int STAGE = decltype(stage_c)::value;
+            constexpr bool MASKED = decltype(masked_c)::value, FIRST = decltype(first_c)::value;
+            const unsigned char* ks = smem + STAGE * STAGE_BYTES;
+            const unsigned char* vs = ks + TILE_BYTES;
+            const int start = t * BN;
+            wait_vmem();
+            __syncthreads();
+            // Branch-free prefetch: the last tile re-fetches itself into the idle stage.
+            issue(min(t + 1, ntiles - 1), STAGE ^ 1);
+            // P1
+            load_k<BN, MASKED, CAUSAL>(ks, off, kr, start, a.sk, qb);
+            qk_regs<BN, MASKED, CAUSAL>(kr, qra, s_a, start, a.sk, qa);
+            if constexpr (!FIRST) softmax_tail<BN, LSE>(s_b, p_b, sb, cb, scale2);
+            // P2
+            if constexpr (!FIRST) {
+                apply_rescale(sb, cb);
+                pv_regs<BN, MASKED, CAUSAL>(vr, p_b, sb, start - BN, a.sk, qb);
+            }
+            softmax_head<BN, MASKED, CAUSAL, LSE>(s_a, p_a, sa, ca, FIRST, start, a.sk, qa, row_a, half, scale2);
+            // P3
+            qk_regs<BN, MASKED, CAUSAL>(kr, qrb, s_b, start, a.sk, qb);
+            softmax_tail<BN, LSE>(s_a, p_a, sa, ca, scale2);
+            // P4
+            apply_rescale(sa, ca);
+            load_v<BN, MASKED, CAUSAL>(vs, off, vr, start, a.sk, qb);
+            pv_regs<BN, MASKED, CAUSAL>(vr, p_a, sa, start, a.sk, qa);
+            softmax_head<BN, MASKED, CAUSAL, LSE>(s_b, p_b, sb, cb, FIRST, start, a.sk, qb, row_b, half, scale2);
+        };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using Plain = std::integral_constant<bool, false>;
+        using Masked = std::integral_constant<bool, true>;
+        using First = std::integral_constant<bool, true>;
+        using Later = std::integral_constant<bool, false>;
+        if (nfull > 0) iter(S0{}, Plain{}, First{}, 0);
+        else iter(S0{}, Masked{}, First{}, 0);
+        int t = 1;
+        for (; t + 1 < nfull; t += 2) {
+            iter(S1{}, Plain{}, Later{}, t);
+            iter(S0{}, Plain{}, Later{}, t + 1);
+        }
+        for (; t < ntiles; ++t) {
+            // At most one plain tile and the masked ones remain; the masked
+            // body is correct for plain tiles too.
+            if (t & 1) iter(S1{}, Masked{}, Later{}, t);
+            else iter(S0{}, Masked{}, Later{}, t);
+        }
+        // Drain: group B still owes softmax tail + PV of the last tile.
+        softmax_tail<BN, LSE>(s_b, p_b, sb, cb, scale2);
+        apply_rescale(sb, cb);
+        pv_regs<BN, true, CAUSAL>(vr, p_b, sb, (ntiles - 1) * BN, a.sk, qb);
+
+        // Epilogue (both groups): O = acc / lb in BF16, LSE = m*ln2 + ln(l).
+        const uint32_t obase = uint32_t(wave * 64 + col) * row_bytes + half * 8;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const RowState& st = g ? sb : sa;
+            const float inv = 1.f / st.lb;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+#pragma unroll
+                for (int vg = 0; vg < 4; ++vg) {
+                    const f32x2 x0 = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv};
+                    const f32x2 x1 = {st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
+                    const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
+                    const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
+                    store8(ro, obase + g * 32 * row_bytes + (db * 32 + vg * 8) * 2,
+                           bf16x4{y0[0], y0[1], y1[0], y1[1]});
+                }
+            }
+            if constexpr (LSE) {
+                const int row = g ? row_b : row_a;
+                if (half == 0 && row < a.sq) a.lse[int64_t(bh) * a.sq + row] = st.m * LN2 + logf(st.l);
+            }
+        }
+        __syncthreads();   // LDS stages are reused by the next work item
+    };
+    for_each_item<CAUSAL>(tiles, total, process);
 }
 
 }  // namespace fav4
