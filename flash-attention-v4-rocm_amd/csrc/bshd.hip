@@ -61,13 +61,14 @@ int dispatch(const Fav4Args& a, int config, hipStream_t stream) {
 
 // Replaces src/bshd.hip:23-25.  Small query lengths use 128-row workgroups so
 // short sequences still spread over the 256 CUs; everything else uses 256 rows.
-extern "C" int fav4_bshd_select_config(const Fav4Args* a) {
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_select_config(const Fav4Args* a) {
     if (!a) return -1;
     return a->sq < 256 ? 1 : 2;
 }
 
 // Replaces src/bshd.hip:26-38.
-extern "C" int fav4_bshd_forward(const Fav4Args* a, int causal, int config, hipStream_t stream) {
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward(const Fav4Args* a, int causal, int config,
+                                                                hipStream_t stream) {
     if (!a || !a->q || !a->k || !a->v || !a->o || a->batch <= 0 || a->heads <= 0 || a->sq <= 0 ||
         a->sk <= 0 || (causal != 0 && causal != 1) || config < 0 || config > 3 ||
         !std::isfinite(a->scale) || a->scale <= 0)

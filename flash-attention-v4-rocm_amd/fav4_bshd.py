@@ -23,7 +23,7 @@ INCLUDE = ROOT / "include"
 D = 128
 
 HIPCC_FLAGS = [
-    "-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-shared",
+    "-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-shared", "-fvisibility=hidden",
     f"-I{INCLUDE}", f"-I{CSRC}",
     "-fgpu-flush-denormals-to-zero",
     # keep the compiler from emitting packed-FP32 VALU ops (v_pk_fma_f32 & co.)

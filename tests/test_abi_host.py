@@ -1,0 +1,126 @@
+"""Host-only checks of the C ABI (no GPU needed, no compute call is made).
+
+The library must export exactly the two entry points of the reference header
+(include/fav4_bshd.h:19-20), lay out Fav4Args byte for byte like it
+(include/fav4_bshd.h:4-10), and reject bad arguments with
+hipErrorInvalidValue before touching HIP, as src/bshd.hip:27-34 does.
+"""
+import ctypes as C
+import math
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from tests.conftest import ROOT, load_package
+
+HIP_ERROR_INVALID_VALUE = 1
+HEADER = ROOT / "include" / "fav4_bshd.h"
+
+# Offsets of the reference argument block (5 pointers, 4 ints, 1 float).
+LAYOUT = dict(q=0, k=8, v=16, o=24, lse=32, batch=40, heads=44, sq=48, sk=52, scale=56)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    pkg = load_package()
+    if not pkg.LIB_PATH.exists():
+        pkg.build_library()
+    return pkg.load_library()
+
+
+@pytest.fixture(scope="module")
+def Args():
+    return load_package().Args
+
+
+def test_exports_exactly_the_c_abi():
+    pkg = load_package()
+    if not pkg.LIB_PATH.exists():
+        pkg.build_library()
+    out = subprocess.run(["nm", "-D", "--defined-only", str(pkg.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    names = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    public = {n for n in names if not n.startswith("_")}
+    assert public == {"fav4_bshd_forward", "fav4_bshd_select_config"}, public
+
+
+def test_ctypes_layout_matches_reference(Args):
+    assert C.sizeof(Args) == 64
+    for name, offset in LAYOUT.items():
+        assert getattr(Args, name).offset == offset, name
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_header_layout_compiled(tmp_path):
+    """Compile the public header with the host compiler and read the layout."""
+    src = tmp_path / "layout.cpp"
+    fields = ", ".join(f'offsetof(Fav4Args, {n})' for n in LAYOUT)
+    src.write_text(
+        '#include <cstddef>\n#include <cstdio>\n#include "fav4_bshd.h"\n'
+        'int main() { size_t o[] = {' + fields + '};\n'
+        '  std::printf("%zu", sizeof(Fav4Args)); for (size_t x : o) std::printf(" %zu", x); }\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", f"-I{HEADER.parent}", "-I/opt/rocm/include",
+                    str(src), "-o", str(exe)], check=True, capture_output=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got == [64] + list(LAYOUT.values())
+
+
+def _good(Args):
+    # Distinct, 16-byte aligned fake device addresses; never dereferenced here
+    # because every call below carries exactly one invalid field.
+    return dict(q=0x10000, k=0x20000, v=0x30000, o=0x40000, lse=None, batch=2, heads=4, sq=256, sk=256,
+                scale=1 / math.sqrt(128))
+
+
+BAD = [
+    ("q_null", dict(q=None)), ("k_null", dict(k=None)), ("v_null", dict(v=None)), ("o_null", dict(o=None)),
+    ("batch0", dict(batch=0)), ("heads0", dict(heads=0)), ("sq0", dict(sq=0)), ("sk0", dict(sk=0)),
+    ("batch_neg", dict(batch=-3)), ("sk_neg", dict(sk=-1)),
+    ("scale0", dict(scale=0.0)), ("scale_neg", dict(scale=-0.5)), ("scale_nan", dict(scale=float("nan"))),
+    ("scale_inf", dict(scale=float("inf"))),
+    ("bh_overflow", dict(batch=1 << 16, heads=1 << 16)), ("heads_overflow", dict(heads=1 << 24)),
+    ("sq_overflow", dict(heads=8, sq=1 << 21)), ("sk_overflow", dict(heads=8, sk=1 << 21)),
+    ("q_misaligned", dict(q=0x10002)), ("k_misaligned", dict(k=0x20008)), ("v_misaligned", dict(v=0x30004)),
+    ("o_misaligned", dict(o=0x40001)),
+]
+
+
+@pytest.mark.parametrize("name,change", BAD, ids=[b[0] for b in BAD])
+def test_rejects_bad_arguments(lib, Args, name, change):
+    fields = _good(Args)
+    fields.update(change)
+    a = Args(**fields)
+    assert lib.fav4_bshd_forward(C.byref(a), 0, 0, None) == HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.parametrize("causal,config", [(-1, 0), (2, 0), (0, -1), (0, 4), (1, 7)])
+def test_rejects_bad_causal_or_config(lib, Args, causal, config):
+    a = Args(**_good(Args))
+    assert lib.fav4_bshd_forward(C.byref(a), causal, config, None) == HIP_ERROR_INVALID_VALUE
+
+
+def test_rejects_null_args(lib):
+    assert lib.fav4_bshd_forward(None, 0, 0, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_select_config(None) == -1
+
+
+@pytest.mark.parametrize("sq,want", [(1, 1), (127, 1), (255, 1), (256, 2), (1000, 2), (4096, 2), (32768, 2)])
+def test_select_config(lib, Args, sq, want):
+    fields = _good(Args)
+    fields["sq"] = sq
+    got = lib.fav4_bshd_select_config(C.byref(Args(**fields)))
+    assert got == want and 1 <= got <= 3
+
+
+def test_runner_rejects_host_tensors():
+    torch = pytest.importorskip("torch")
+    pkg = load_package()
+    runner = pkg.Runner.__new__(pkg.Runner)  # no library needed for the argument checks
+    q = torch.zeros(1, 4, 1, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        runner.args(q, q, q, q, None)
+    with pytest.raises(AssertionError):
+        runner.args(q.float(), q, q, q, None)
