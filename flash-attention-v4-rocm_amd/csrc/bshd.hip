@@ -52,7 +52,7 @@ int dispatch(const Fav4Args& a, int config, hipStream_t stream) {
     switch (config) {
     case 1: return launch<4, 64, 2, false, CAUSAL>(a, stream);
     case 2: return launch<8, 64, 2, false, CAUSAL>(a, stream);
-    case 3: return launch<8, 64, 3, true, CAUSAL>(a, stream);
+    case 3: return launch_g2<32, CAUSAL>(a, stream);
     default: return hipErrorInvalidValue;
     }
 }

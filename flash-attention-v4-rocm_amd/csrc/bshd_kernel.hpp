@@ -142,33 +142,31 @@ __device__ __forceinline__ void tile_mask(f32x16 (&s)[BN / 32], int start, int s
     }
 }
 
-// P = exp2(s*scale2 - m) for one 32-key block, as two BF16 MFMA B operands.
+// P = exp2(s*scale2 - m) for one 16-key unit (half of a 32-key block), as
+// one BF16 MFMA B operand.
 template <bool LSE>
-__device__ __forceinline__ void exp_block(const f32x16& s, bf16x8 (&p)[2], SmCarry& c, float scale2) {
+__device__ __forceinline__ void exp_unit(const f32x16& s, int sub, bf16x8& p, SmCarry& c, float scale2) {
+    f32x2 e[4];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-        f32x2 e[4];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float x = exp2_native(fmaf(s[sub * 8 + i], scale2, c.neg));
-            e[i >> 1][i & 1] = x;
-            if constexpr (LSE) c.part[i & 3] += x;
-        }
-        const bf16x2 b0 = __builtin_convertvector(e[0], bf16x2);
-        const bf16x2 b1 = __builtin_convertvector(e[1], bf16x2);
-        const bf16x2 b2 = __builtin_convertvector(e[2], bf16x2);
-        const bf16x2 b3 = __builtin_convertvector(e[3], bf16x2);
-        c.pb0 = bf16_pair_sum(b0, c.pb0);
-        c.pb1 = bf16_pair_sum(b1, c.pb1);
-        c.pb0 = bf16_pair_sum(b2, c.pb0);
-        c.pb1 = bf16_pair_sum(b3, c.pb1);
-        p[sub] = bf16x8{b0[0], b0[1], b1[0], b1[1], b2[0], b2[1], b3[0], b3[1]};
+    for (int i = 0; i < 8; ++i) {
+        const float x = exp2_native(fmaf(s[sub * 8 + i], scale2, c.neg));
+        e[i >> 1][i & 1] = x;
+        if constexpr (LSE) c.part[i & 3] += x;
     }
+    const bf16x2 b0 = __builtin_convertvector(e[0], bf16x2);
+    const bf16x2 b1 = __builtin_convertvector(e[1], bf16x2);
+    const bf16x2 b2 = __builtin_convertvector(e[2], bf16x2);
+    const bf16x2 b3 = __builtin_convertvector(e[3], bf16x2);
+    c.pb0 = bf16_pair_sum(b0, c.pb0);
+    c.pb1 = bf16_pair_sum(b1, c.pb1);
+    c.pb0 = bf16_pair_sum(b2, c.pb0);
+    c.pb1 = bf16_pair_sum(b3, c.pb1);
+    p = bf16x8{b0[0], b0[1], b1[0], b1[1], b2[0], b2[1], b3[0], b3[1]};
 }
 
-// Softmax head: masks, row max, conditional base update (log2 units), P of
-// the first 32-key block.  The O rescale it decides is applied by
-// apply_rescale before the tile's PV product.
+// Softmax head: masks, row max, conditional base update (log2 units), and P
+// of the first half of the tile's 16-key units.  The O rescale it decides is
+// applied by apply_rescale before the tile's PV product.
 template <int BN, bool MASKED, bool CAUSAL, bool LSE>
 __device__ __forceinline__ void softmax_head(f32x16 (&s)[BN / 32], bf16x8 (&p)[BN / 32][2], RowState& st,
                                              SmCarry& c, bool first, int start, int sk, int qw, int row,
@@ -191,23 +189,30 @@ __device__ __forceinline__ void softmax_head(f32x16 (&s)[BN / 32], bf16x8 (&p)[B
     c.pb0 = c.pb1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) c.part[i] = 0.f;
-    exp_block<LSE>(s[0], p[0], c, scale2);
+#pragma unroll
+    for (int u = 0; u < KB; ++u) exp_unit<LSE>(s[u >> 1], u & 1, p[u >> 1][u & 1], c, scale2);
 }
 
-// Softmax tail: P of the remaining blocks, running sums.
+// Softmax tail: P of the remaining units, running sums.
 template <int BN, bool LSE>
 __device__ __forceinline__ void softmax_tail(const f32x16 (&s)[BN / 32], bf16x8 (&p)[BN / 32][2], RowState& st,
                                              SmCarry& c, float scale2) {
+    constexpr int KB = BN / 32;
 #pragma unroll
-    for (int kb = 1; kb < BN / 32; ++kb) exp_block<LSE>(s[kb], p[kb], c, scale2);
+    for (int u = KB; u < 2 * KB; ++u) exp_unit<LSE>(s[u >> 1], u & 1, p[u >> 1][u & 1], c, scale2);
     st.lb = st.lb * c.alpha + xhalf_sum(c.pb0 + c.pb1);
     if constexpr (LSE) st.l = st.l * c.alpha + xhalf_sum((c.part[0] + c.part[1]) + (c.part[2] + c.part[3]));
 }
 
+// One 16-register accumulator block at a time, fenced, so the (AGPR-resident)
+// accumulators need at most 16 VGPR temporaries while being scaled.
 __device__ __forceinline__ void apply_rescale(RowState& st, const SmCarry& c) {
     if (c.rescale) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) st.o[db] *= c.alpha;
+        for (int db = 0; db < 4; ++db) {
+            st.o[db] *= c.alpha;
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 }
 
@@ -245,6 +250,63 @@ __device__ __forceinline__ void tile_pv(const unsigned char* vs, const LdsOffset
             for (int db = 0; db < 4; ++db) st.o[db] = mfma32(vop[db], p[kb][sub], st.o[db]);
         }
     }
+}
+
+// One key tile for one 32-row wave, software pipelined inside the tile:
+//   QK block 0 | QK block 1 (+ mask/max of block 0) | base update
+//   exp(unit 0) | [rescale O] | PV(unit u-1) beside exp(unit u) ... | PV(last)
+// A unit is 16 keys (one PV k-step for all four 32-dim blocks).  Keeping the
+// rare O-rescale branch in front of the first PV leaves the exp/PV overlap in
+// one basic block, where the scheduler can interleave the VALU work of unit u
+// with the MFMAs of unit u-1.
+template <int BN, bool MASKED, bool CAUSAL, bool LSE>
+__device__ __forceinline__ void attend_fused(const unsigned char* ks, const unsigned char* vs, const LdsOffsets& off,
+                                             const bf16x8 (&qr)[8], RowState& st, bool first, int start, int sk,
+                                             int qw, int row, int half, float scale2) {
+    constexpr int KB = BN / 32, U = 2 * KB;
+    f32x16 s[KB];
+    tile_qk<BN, MASKED, CAUSAL>(ks, off, qr, s, start, sk, qw);
+    tile_mask<BN, MASKED, CAUSAL>(s, start, sk, qw, row, half);
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
+    mx = xhalf_max(mx);
+    const float cand = fmaxf(st.m, mx * scale2);
+    const bool update = first || cand > st.m + RESCALE_THRESHOLD;
+    const float next = update ? cand : st.m;
+    SmCarry c;
+    c.alpha = exp2_native(st.m - next);
+    c.rescale = !first && __builtin_amdgcn_ballot_w64(update) != 0;
+    st.m = next;
+    c.neg = -next;
+    c.pb0 = c.pb1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c.part[i] = 0.f;
+    bf16x8 p[U];
+    exp_unit<LSE>(s[0], 0, p[0], c, scale2);
+    apply_rescale(st, c);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int kb = u >> 1;
+        const bool act = block_active<MASKED, CAUSAL>(start + kb * 32, sk, qw);
+        if (u + 1 < U) exp_unit<LSE>(s[(u + 1) >> 1], (u + 1) & 1, p[u + 1], c, scale2);
+        if (!MASKED || act) {
+            const unsigned char* vb = vs + u * 16 * ROW_BYTES;
+            bf16x8 vop[4];
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const bf16x4 lo = lds_read_tr(vb + off.v[0][db]);
+                const bf16x4 hi = lds_read_tr(vb + off.v[1][db]);
+                vop[db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+#pragma unroll
+            for (int db = 0; db < 4; ++db) st.o[db] = mfma32(vop[db], p[u], st.o[db]);
+        }
+    }
+    st.lb = st.lb * c.alpha + xhalf_sum(c.pb0 + c.pb1);
+    if constexpr (LSE) st.l = st.l * c.alpha + xhalf_sum((c.part[0] + c.part[1]) + (c.part[2] + c.part[3]));
 }
 
 // WAVES waves x 32 query rows per workgroup, BN keys per tile, STAGES LDS
@@ -363,9 +425,8 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
             __syncthreads();    // ... and every other wave's; stage (t+1)%STAGES is free
             if (t + 1 < ntiles) issue(t + 1, (STAGE + 1) % STAGES);
             if constexpr (!LAG) {
-                tile_qk<BN, MCUR, CAUSAL>(cur, off, qr, s, t * BN, a.sk, qw);
-                tile_softmax<BN, MCUR, CAUSAL, LSE>(s, p, st, t == 0, t * BN, a.sk, qw, row, half, scale2);
-                tile_pv<BN, MCUR, CAUSAL>(cur + TILE_BYTES, off, p, st, t * BN, a.sk, qw);
+                attend_fused<BN, MCUR, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st, t == 0, t * BN, a.sk, qw,
+                                                    row, half, scale2);
             } else {
                 if (t > 0) {
                     tile_softmax<BN, MPREV, CAUSAL, LSE>(s, p, st, t == 1, (t - 1) * BN, a.sk, qw, row, half,
@@ -516,13 +577,13 @@ __device__ __forceinline__ void pv_regs(const bf16x8 (&vr)[BN / 32][2][4], const
 template <int BN, bool CAUSAL, bool LSE>
 __global__ __launch_bounds__(256)
 void fwd_kernel_g2(Fav4Args a, int tiles, int total) {
-    constexpr int WAVES = 4, BM = 256;
+    constexpr int WAVES = 4, BM = 256, STAGES = 3;
     constexpr int KB = BN / 32;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
     constexpr int STAGE_BYTES = 2 * TILE_BYTES;          // K then V
     constexpr int DMA = BN / 4 / WAVES;                  // 1 KiB DMA ops per wave per matrix
     static_assert(BN % 32 == 0 && BN % (4 * WAVES) == 0, "tile shape");
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[STAGES * STAGE_BYTES];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -569,12 +630,15 @@ void fwd_kernel_g2(Fav4Args a, int tiles, int total) {
         const int ntiles = (kend + BN - 1) / BN;
         const int nfull = (CAUSAL ? min(a.sk, q0 + 1) : a.sk) / BN;
 
-        auto issue = [&](int t, int stage) {
+        // DMA of tile t into stage t % 3.  Tiles past the last are clamped to
+        // it, so the prefetch needs no branch (the copy lands in an idle stage).
+        auto issue = [&](int t) {
+            t = min(t, ntiles - 1);
             const int64_t first = int64_t(t) * BN;
             const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * row_bytes + ROW_BYTES;
             const u32x4 rk = make_desc(kbase + first * row_bytes, bytes);
             const u32x4 rv = make_desc(vbase + first * row_bytes, bytes);
-            const uint32_t ks = smem_base + stage * STAGE_BYTES + wave * DMA * 1024;
+            const uint32_t ks = smem_base + (t % STAGES) * STAGE_BYTES + wave * DMA * 1024;
 #pragma unroll
             for (int i = 0; i < DMA; ++i) {
                 dma16(rk, ks + i * 1024, dk[i]);
@@ -582,7 +646,8 @@ void fwd_kernel_g2(Fav4Args a, int tiles, int total) {
             }
         };
 
-        issue(0, 0);
+        issue(0);
+        issue(1);
         bf16x8 qra[8], qrb[8];
         {
             const uint32_t qoff = uint32_t(wave * 64 + col) * row_bytes + half * 16;
@@ -591,8 +656,10 @@ void fwd_kernel_g2(Fav4Args a, int tiles, int total) {
                 qra[c] = load16(rq, qoff + c * 32);
                 qrb[c] = load16(rq, qoff + 32 * row_bytes + c * 32);
             }
+            // Q lives in AGPRs (MFMA B operands may come from AGPRs on gfx950),
+            // leaving the 256 arch VGPRs to S, P and the K/V operands.
 #pragma unroll
-            for (int c = 0; c < 8; ++c) asm volatile("" ::"v"(qra[c]), "v"(qrb[c]));
+            for (int c = 0; c < 8; ++c) asm volatile("" : "+a"(qra[c]), "+a"(qrb[c]));
         }
         RowState sa, sb;
 #pragma unroll
@@ -611,24 +678,23 @@ void fwd_kernel_g2(Fav4Args a, int tiles, int total) {
             const unsigned char* ks = smem + STAGE * STAGE_BYTES;
             const unsigned char* vs = ks + TILE_BYTES;
             const int start = t * BN;
-            wait_vmem();
+            wait_vmem_keep<2 * DMA>();   // tile t landed; tile t+1 may still be in flight
             __syncthreads();
-            // Branch-free prefetch: the last tile re-fetches itself into the idle stage.
-            issue(min(t + 1, ntiles - 1), STAGE ^ 1);
-            // P1
+            issue(t + 2);
+            // P1: load K(t); QK_A(t) | softmax tail B(t-1)
             load_k<BN, MASKED, CAUSAL>(ks, off, kr, start, a.sk, qb);
             qk_regs<BN, MASKED, CAUSAL>(kr, qra, s_a, start, a.sk, qa);
             if constexpr (!FIRST) softmax_tail<BN, LSE>(s_b, p_b, sb, cb, scale2);
-            // P2
+            // P2: PV_B(t-1) | softmax head A(t)
             if constexpr (!FIRST) {
                 apply_rescale(sb, cb);
                 pv_regs<BN, MASKED, CAUSAL>(vr, p_b, sb, start - BN, a.sk, qb);
             }
             softmax_head<BN, MASKED, CAUSAL, LSE>(s_a, p_a, sa, ca, FIRST, start, a.sk, qa, row_a, half, scale2);
-            // P3
+            // P3: QK_B(t) | softmax tail A(t)
             qk_regs<BN, MASKED, CAUSAL>(kr, qrb, s_b, start, a.sk, qb);
             softmax_tail<BN, LSE>(s_a, p_a, sa, ca, scale2);
-            // P4
+            // P4: load V(t); PV_A(t) | softmax head B(t)
             apply_rescale(sa, ca);
             load_v<BN, MASKED, CAUSAL>(vs, off, vr, start, a.sk, qb);
             pv_regs<BN, MASKED, CAUSAL>(vr, p_a, sa, start, a.sk, qa);
@@ -636,6 +702,7 @@ void fwd_kernel_g2(Fav4Args a, int tiles, int total) {
         };
         using S0 = std::integral_constant<int, 0>;
         using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
         using Plain = std::integral_constant<bool, false>;
         using Masked = std::integral_constant<bool, true>;
         using First = std::integral_constant<bool, true>;
@@ -643,15 +710,17 @@ void fwd_kernel_g2(Fav4Args a, int tiles, int total) {
         if (nfull > 0) iter(S0{}, Plain{}, First{}, 0);
         else iter(S0{}, Masked{}, First{}, 0);
         int t = 1;
-        for (; t + 1 < nfull; t += 2) {
+        for (; t + 2 < nfull; t += 3) {
             iter(S1{}, Plain{}, Later{}, t);
-            iter(S0{}, Plain{}, Later{}, t + 1);
+            iter(S2{}, Plain{}, Later{}, t + 1);
+            iter(S0{}, Plain{}, Later{}, t + 2);
         }
         for (; t < ntiles; ++t) {
-            // At most one plain tile and the masked ones remain; the masked
-            // body is correct for plain tiles too.
-            if (t & 1) iter(S1{}, Masked{}, Later{}, t);
-            else iter(S0{}, Masked{}, Later{}, t);
+            // The masked body is correct for the (at most two) plain tiles left too.
+            const int r = t % 3;
+            if (r == 0) iter(S0{}, Masked{}, Later{}, t);
+            else if (r == 1) iter(S1{}, Masked{}, Later{}, t);
+            else iter(S2{}, Masked{}, Later{}, t);
         }
         // Drain: group B still owes softmax tail + PV of the last tile.
         softmax_tail<BN, LSE>(s_b, p_b, sb, cb, scale2);
@@ -681,7 +750,8 @@ void fwd_kernel_g2(Fav4Args a, int tiles, int total) {
                 if (half == 0 && row < a.sq) a.lse[int64_t(bh) * a.sq + row] = st.m * LN2 + logf(st.l);
             }
         }
-        __syncthreads();   // LDS stages are reused by the next work item
+        wait_vmem();       // the clamped prefetches have landed before the stages are reused
+        __syncthreads();
     };
     for_each_item<CAUSAL>(tiles, total, process);
 }

@@ -76,6 +76,13 @@ __device__ __forceinline__ void dma16(u32x4 desc, uint32_t lds, uint32_t voffset
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Wait until at most N vector-memory ops of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmem_keep() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 __device__ __forceinline__ bf16x8 load16(rsrc_t r, uint32_t voffset) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0));
 }
