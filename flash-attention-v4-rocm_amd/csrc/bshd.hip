@@ -15,7 +15,7 @@ namespace {
 // Upper bound on launched workgroups; larger problems loop inside the kernel.
 constexpr int64_t MAX_GRID = int64_t(1) << 22;
 
-template <int WAVES, int BN, int STAGES, bool PINGPONG, bool CAUSAL>
+template <int WAVES, int BN, int STAGES, bool PIPE, bool CAUSAL>
 int launch(const Fav4Args& a, hipStream_t stream) {
     constexpr int BM = WAVES * 32;
     const int tiles = (a.sq + BM - 1) / BM;
@@ -23,27 +23,11 @@ int launch(const Fav4Args& a, hipStream_t stream) {
     if (total > INT_MAX) return hipErrorInvalidValue;
     const int grid = int(total < MAX_GRID ? total : MAX_GRID);
     if (a.lse)
-        hipLaunchKernelGGL((fav4::fwd_kernel<WAVES, BN, CAUSAL, true, STAGES, PINGPONG>), dim3(grid),
+        hipLaunchKernelGGL((fav4::fwd_kernel<WAVES, BN, CAUSAL, true, STAGES, PIPE>), dim3(grid),
                            dim3(WAVES * 64), 0, stream, a, tiles, int(total));
     else
-        hipLaunchKernelGGL((fav4::fwd_kernel<WAVES, BN, CAUSAL, false, STAGES, PINGPONG>), dim3(grid),
+        hipLaunchKernelGGL((fav4::fwd_kernel<WAVES, BN, CAUSAL, false, STAGES, PIPE>), dim3(grid),
                            dim3(WAVES * 64), 0, stream, a, tiles, int(total));
-    return hipGetLastError();
-}
-
-template <int BN, bool CAUSAL>
-int launch_g2(const Fav4Args& a, hipStream_t stream) {
-    constexpr int BM = 256;
-    const int tiles = (a.sq + BM - 1) / BM;
-    const int64_t total = int64_t(fav4::items_per_head<CAUSAL>(tiles)) * a.batch * a.heads;
-    if (total > INT_MAX) return hipErrorInvalidValue;
-    const int grid = int(total < MAX_GRID ? total : MAX_GRID);
-    if (a.lse)
-        hipLaunchKernelGGL((fav4::fwd_kernel_g2<BN, CAUSAL, true>), dim3(grid), dim3(256), 0, stream, a, tiles,
-                           int(total));
-    else
-        hipLaunchKernelGGL((fav4::fwd_kernel_g2<BN, CAUSAL, false>), dim3(grid), dim3(256), 0, stream, a, tiles,
-                           int(total));
     return hipGetLastError();
 }
 
@@ -52,7 +36,7 @@ int dispatch(const Fav4Args& a, int config, hipStream_t stream) {
     switch (config) {
     case 1: return launch<4, 64, 2, false, CAUSAL>(a, stream);
     case 2: return launch<8, 64, 2, false, CAUSAL>(a, stream);
-    case 3: return launch_g2<32, CAUSAL>(a, stream);
+    case 3: return launch<8, 64, 3, true, CAUSAL>(a, stream);
     default: return hipErrorInvalidValue;
     }
 }

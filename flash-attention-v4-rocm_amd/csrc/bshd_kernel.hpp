@@ -265,7 +265,12 @@ __device__ __forceinline__ void attend_fused(const unsigned char* ks, const unsi
                                              int qw, int row, int half, float scale2) {
     constexpr int KB = BN / 32, U = 2 * KB;
     f32x16 s[KB];
+    // Raised issue priority while this wave feeds QK^T MFMAs: when the two
+    // waves of a SIMD compete, the one in its MFMA phase goes first and the
+    // other fills the VALU slots (measured +5% at B32H8S4096).
+    __builtin_amdgcn_s_setprio(1);
     tile_qk<BN, MASKED, CAUSAL>(ks, off, qr, s, start, sk, qw);
+    __builtin_amdgcn_s_setprio(0);
     tile_mask<BN, MASKED, CAUSAL>(s, start, sk, qw, row, half);
     float mx = -__builtin_inff();
 #pragma unroll
@@ -309,29 +314,82 @@ __device__ __forceinline__ void attend_fused(const unsigned char* ks, const unsi
     if constexpr (LSE) st.l = st.l * c.alpha + xhalf_sum((c.part[0] + c.part[1]) + (c.part[2] + c.part[3]));
 }
 
+// Row max of one tile's raw logits, combined over the two lane halves.
+template <int BN>
+__device__ __forceinline__ float tile_rowmax(const f32x16 (&s)[BN / 32]) {
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
+    return xhalf_max(mx);
+}
+
+// Base update from a precomputed row max, then all of the tile's P units and
+// the running sums.  The O rescale it decides is applied by apply_rescale.
+template <int BN, bool LSE>
+__device__ __forceinline__ void softmax_from_max(const f32x16 (&s)[BN / 32], float mx, bf16x8 (&p)[2 * (BN / 32)],
+                                                 RowState& st, SmCarry& c, bool first, float scale2) {
+    constexpr int U = 2 * (BN / 32);
+    const float cand = fmaxf(st.m, mx * scale2);
+    const bool update = first || cand > st.m + RESCALE_THRESHOLD;
+    const float next = update ? cand : st.m;
+    c.alpha = exp2_native(st.m - next);
+    c.rescale = !first && __builtin_amdgcn_ballot_w64(update) != 0;
+    st.m = next;
+    c.neg = -next;
+    c.pb0 = c.pb1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c.part[i] = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) exp_unit<LSE>(s[u >> 1], u & 1, p[u], c, scale2);
+    st.lb = st.lb * c.alpha + xhalf_sum(c.pb0 + c.pb1);
+    if constexpr (LSE) st.l = st.l * c.alpha + xhalf_sum((c.part[0] + c.part[1]) + (c.part[2] + c.part[3]));
+}
+
+// O^T += V^T.P^T for an unmasked tile.
+template <int BN>
+__device__ __forceinline__ void pv_plain(const unsigned char* vs, const LdsOffsets& off,
+                                         const bf16x8 (&p)[2 * (BN / 32)], RowState& st) {
+#pragma unroll
+    for (int u = 0; u < 2 * (BN / 32); ++u) {
+        const unsigned char* vb = vs + u * 16 * ROW_BYTES;
+        bf16x8 vop[4];
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const bf16x4 lo = lds_read_tr(vb + off.v[0][db]);
+            const bf16x4 hi = lds_read_tr(vb + off.v[1][db]);
+            vop[db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+#pragma unroll
+        for (int db = 0; db < 4; ++db) st.o[db] = mfma32(vop[db], p[u], st.o[db]);
+    }
+}
+
 // WAVES waves x 32 query rows per workgroup, BN keys per tile, STAGES LDS
-// buffers of K+V.  PINGPONG (8 waves, 3 stages): waves 0-3 run QK(t),
-// softmax(t), PV(t) between barriers t and t+1 while waves 4-7 (one of each
-// group per SIMD) run softmax(t-1), PV(t-1), QK(t), so one wave's softmax
-// VALU work overlaps the other wave's MFMAs on the same SIMD.  Tile t lives
-// in stage t % STAGES; the DMA of tile t+1 is issued right after barrier t
-// into the stage that tile t-2 used (read before barrier t by everyone).
-template <int WAVES, int BN, bool CAUSAL, bool LSE, int STAGES, bool PINGPONG>
-__global__ __launch_bounds__(WAVES * 64)
+// buffers of K+V.  Tile t lives in stage t % STAGES; its DMA is issued
+// STAGES-1 tiles ahead (right after barrier t-STAGES+1, into the stage that
+// tile t-STAGES used, which every wave finished reading before that barrier).
+// PIPE (3 stages): unmasked key tiles run software pipelined across tiles,
+// QK^T(t+1) beside softmax(t) and PV(t) beside the row max of tile t+1, so
+// each wave always has MFMA and VALU work in flight.  K(t+1) and V(t) are
+// both read between barriers t and t+1; the DMA of tile t+2 goes to the third
+// stage.  Masked tiles (causal diagonal, key tail) follow unpipelined.
+template <int WAVES, int BN, bool CAUSAL, bool LSE, int STAGES, bool PIPE = false>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel(Fav4Args a, int tiles, int total) {
+    static_assert(!PIPE || STAGES == 3, "the cross-tile pipeline keeps three tiles in LDS");
     constexpr int BM = WAVES * 32;
-    constexpr int KB = BN / 32;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
     constexpr int STAGE_BYTES = 2 * TILE_BYTES;          // K then V
     constexpr int DMA = BN / 4 / WAVES;                  // 1 KiB DMA ops per wave per matrix
+    constexpr int AHEAD = STAGES - 1;                    // prefetch distance in tiles
     static_assert(BN % 32 == 0 && BN % (4 * WAVES) == 0, "tile shape");
-    static_assert(!PINGPONG || (WAVES == 8 && STAGES == 3), "ping-pong needs two 4-wave groups, 3 stages");
     static_assert(STAGES == 2 || STAGES == 3, "stages");
     __shared__ __attribute__((aligned(1024))) unsigned char smem[STAGES * STAGE_BYTES];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const bool lagging = PINGPONG && wave >= 4;           // group that runs half a tile behind
     const int col = lane & 31, half = lane >> 5;
     const uint32_t row_bytes = uint32_t(a.heads) * ROW_BYTES;   // stride between sequence positions
     const float scale2 = a.scale * LOG2E;
@@ -374,16 +432,21 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
                                     uint32_t(a.sq - q0 - 1) * row_bytes + ROW_BYTES);
         // Key tiles: [0, nfull) are unmasked for every row of the workgroup,
         // [nfull, ntiles) cross the key tail or the causal diagonal.
+        constexpr int BNT = BN;                           // keys per LDS tile
         const int kend = CAUSAL ? min(a.sk, q0 + BM) : a.sk;
-        const int ntiles = (kend + BN - 1) / BN;
-        const int nfull = (CAUSAL ? min(a.sk, q0 + 1) : a.sk) / BN;
+        const int ntiles = (kend + BNT - 1) / BNT;
+        const int nfull = (CAUSAL ? min(a.sk, q0 + 1) : a.sk) / BNT;
 
-        auto issue = [&](int t, int stage) {
-            const int64_t first = int64_t(t) * BN;
+        // DMA of tile t into stage t % STAGES.  Tiles past the last one are
+        // clamped to it (the copy lands in a stage nobody reads any more), so
+        // the prefetch needs no branch and vmcnt bookkeeping stays uniform.
+        auto issue = [&](int t) {
+            const int tc = min(t, ntiles - 1);
+            const int64_t first = int64_t(tc) * BNT;
             const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * row_bytes + ROW_BYTES;
             const u32x4 rk = make_desc(kbase + first * row_bytes, bytes);
             const u32x4 rv = make_desc(vbase + first * row_bytes, bytes);
-            const uint32_t ks = smem_base + stage * STAGE_BYTES + wave * DMA * 1024;
+            const uint32_t ks = smem_base + (t % STAGES) * STAGE_BYTES + wave * DMA * 1024;
 #pragma unroll
             for (int i = 0; i < DMA; ++i) {
                 dma16(rk, ks + i * 1024, dk[i]);
@@ -391,14 +454,15 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
             }
         };
 
-        issue(0, 0);
+#pragma unroll
+        for (int t = 0; t < AHEAD; ++t) issue(t);   // PIPE: tiles 0 and 1
         bf16x8 qr[8];
         {
             const uint32_t qoff = uint32_t(wave * 32 + col) * row_bytes + half * 16;
 #pragma unroll
             for (int c = 0; c < 8; ++c) qr[c] = load16(rq, qoff + c * 32);
             // Retire the Q loads here, so that inside the key loop the only
-            // outstanding vector-memory ops are the K/V DMA of the next tile.
+            // outstanding vector-memory ops are K/V DMAs.
 #pragma unroll
             for (int c = 0; c < 8; ++c) asm volatile("" ::"v"(qr[c]));
         }
@@ -408,74 +472,120 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
         st.m = -__builtin_inff();
         st.lb = 0.f;
         st.l = 0.f;
-        f32x16 s[KB];
-        bf16x8 p[KB][2];
 
-        // One pipeline step on compile-time stages: wait for tile t, prefetch
-        // tile t+1, then this wave's share of the work between two barriers.
-        // LAG selects the lagging group's order (softmax+PV of t-1, then QK of t).
-        auto step = [&](auto lag_c, auto stage_c, auto mprev_c, auto mcur_c, int t) {
-            constexpr bool LAG = decltype(lag_c)::value;
+        // One pipeline step on a compile-time stage: wait for tile t (the
+        // AHEAD-1 younger tiles may stay in flight), prefetch tile t+AHEAD,
+        // then attend to tile t.
+        auto step = [&](auto stage_c, auto masked_c, int t) {
             constexpr int STAGE = decltype(stage_c)::value;
-            constexpr int PREV = (STAGE + STAGES - 1) % STAGES;
-            constexpr bool MPREV = decltype(mprev_c)::value, MCUR = decltype(mcur_c)::value;
+            constexpr bool MASKED = decltype(masked_c)::value;
             const unsigned char* cur = smem + STAGE * STAGE_BYTES;
-            const unsigned char* prv = smem + PREV * STAGE_BYTES;
-            wait_vmem();        // this wave's DMA of tile t has landed
-            __syncthreads();    // ... and every other wave's; stage (t+1)%STAGES is free
-            if (t + 1 < ntiles) issue(t + 1, (STAGE + 1) % STAGES);
-            if constexpr (!LAG) {
-                attend_fused<BN, MCUR, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st, t == 0, t * BN, a.sk, qw,
-                                                    row, half, scale2);
-            } else {
-                if (t > 0) {
-                    tile_softmax<BN, MPREV, CAUSAL, LSE>(s, p, st, t == 1, (t - 1) * BN, a.sk, qw, row, half,
-                                                         scale2);
-                    tile_pv<BN, MPREV, CAUSAL>(prv + TILE_BYTES, off, p, st, (t - 1) * BN, a.sk, qw);
-                }
-                tile_qk<BN, MCUR, CAUSAL>(cur, off, qr, s, t * BN, a.sk, qw);
-            }
+            wait_vmem_keep<2 * DMA * (AHEAD - 1)>();
+            __syncthreads();
+            issue(t + AHEAD);
+            attend_fused<BN, MASKED, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st, t == 0, t * BN, a.sk, qw,
+                                                  row, half, scale2);
         };
         using S0 = std::integral_constant<int, 0>;
         using S1 = std::integral_constant<int, 1>;
         using S2 = std::integral_constant<int, 2>;
         using Plain = std::integral_constant<bool, false>;
         using Masked = std::integral_constant<bool, true>;
-        // The whole key loop of one group (both groups run the same barriers).
-        auto key_loop = [&](auto lag_c) {
-            int t = 0;
-            if constexpr (STAGES == 2) {
-                for (; t + 1 < nfull; t += 2) {
-                    step(lag_c, S0{}, Plain{}, Plain{}, t);
-                    step(lag_c, S1{}, Plain{}, Plain{}, t + 1);
+        int t = 0;
+        if constexpr (PIPE) {
+            if (nfull > 6) {
+                f32x16 sa[BN / 32], sb[BN / 32];
+                bf16x8 p[2 * (BN / 32)];
+                SmCarry c;
+                wait_vmem();
+                __syncthreads();
+                tile_qk<BN, false, CAUSAL>(smem, off, qr, sa, 0, a.sk, qw);
+                float mx = tile_rowmax<BN>(sa);
+                // Pipelined tile t (stage STAGE = t%3): S(t) in `cur`, QK^T(t+1)
+                // into `nxt` from stage (t+1)%3, then PV(t).
+                auto pstep = [&](auto stage_c, f32x16 (&cur)[BN / 32], f32x16 (&nxt)[BN / 32], int t) {
+                    constexpr int STAGE = decltype(stage_c)::value;
+                    const unsigned char* here = smem + STAGE * STAGE_BYTES;
+                    const unsigned char* ahead = smem + ((STAGE + 1) % 3) * STAGE_BYTES;
+                    wait_vmem();        // tile t+1 has landed (issued one tile ago)
+                    __syncthreads();
+                    issue(t + 2);
+                    __builtin_amdgcn_s_setprio(1);
+                    tile_qk<BN, false, CAUSAL>(ahead, off, qr, nxt, (t + 1) * BN, a.sk, qw);
+                    __builtin_amdgcn_s_setprio(0);
+                    softmax_from_max<BN, LSE>(cur, mx, p, st, c, t == 0, scale2);
+                    apply_rescale(st, c);
+                    pv_plain<BN>(here + TILE_BYTES, off, p, st);
+                    mx = tile_rowmax<BN>(nxt);
+                };
+                using P0 = std::integral_constant<int, 0>;
+                using P1 = std::integral_constant<int, 1>;
+                using P2 = std::integral_constant<int, 2>;
+                for (; t + 6 < nfull; t += 6) {
+                    pstep(P0{}, sa, sb, t);
+                    pstep(P1{}, sb, sa, t + 1);
+                    pstep(P2{}, sa, sb, t + 2);
+                    pstep(P0{}, sb, sa, t + 3);
+                    pstep(P1{}, sa, sb, t + 4);
+                    pstep(P2{}, sb, sa, t + 5);
                 }
-                for (; t < ntiles; ++t) {
-                    if (t & 1) step(lag_c, S1{}, Masked{}, Masked{}, t);
-                    else step(lag_c, S0{}, Masked{}, Masked{}, t);
-                }
-            } else {
-                for (; t + 2 < nfull; t += 3) {
-                    step(lag_c, S0{}, Plain{}, Plain{}, t);
-                    step(lag_c, S1{}, Plain{}, Plain{}, t + 1);
-                    step(lag_c, S2{}, Plain{}, Plain{}, t + 2);
-                }
-                for (; t < ntiles; ++t) {
-                    const int r = t % 3;
-                    if (r == 0) step(lag_c, S0{}, Masked{}, Masked{}, t);
-                    else if (r == 1) step(lag_c, S1{}, Masked{}, Masked{}, t);
-                    else step(lag_c, S2{}, Masked{}, Masked{}, t);
+                // Drain tile t (t % 3 == 0): K already consumed, V in stage 0.
+                softmax_from_max<BN, LSE>(sa, mx, p, st, c, t == 0, scale2);
+                apply_rescale(st, c);
+                pv_plain<BN>(smem + TILE_BYTES, off, p, st);
+                ++t;
+            }
+            // Remaining tiles, unpipelined, prefetch distance 1 (stage t%3).
+            for (; t < ntiles; ++t) {
+                const int r = t % 3;
+                const bool plain = t < nfull;
+                auto mstep = [&](auto stage_c, auto masked_c) {
+                    constexpr int STAGE = decltype(stage_c)::value;
+                    const unsigned char* cur = smem + STAGE * STAGE_BYTES;
+                    wait_vmem();
+                    __syncthreads();
+                    issue(t + 1);
+                    attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st,
+                                                                             t == 0, t * BN, a.sk, qw, row, half,
+                                                                             scale2);
+                };
+                using M0 = std::integral_constant<int, 0>;
+                using M1 = std::integral_constant<int, 1>;
+                using M2 = std::integral_constant<int, 2>;
+                using Pl = std::integral_constant<bool, false>;
+                using Mk = std::integral_constant<bool, true>;
+                if (plain) {
+                    if (r == 0) mstep(M0{}, Pl{});
+                    else if (r == 1) mstep(M1{}, Pl{});
+                    else mstep(M2{}, Pl{});
+                } else {
+                    if (r == 0) mstep(M0{}, Mk{});
+                    else if (r == 1) mstep(M1{}, Mk{});
+                    else mstep(M2{}, Mk{});
                 }
             }
-            if constexpr (decltype(lag_c)::value) {
-                // The lagging group still owes softmax + PV of the last tile.
-                const int tl = ntiles - 1;
-                const unsigned char* vlast = smem + (tl % STAGES) * STAGE_BYTES + TILE_BYTES;
-                tile_softmax<BN, true, CAUSAL, LSE>(s, p, st, tl == 0, tl * BN, a.sk, qw, row, half, scale2);
-                tile_pv<BN, true, CAUSAL>(vlast, off, p, st, tl * BN, a.sk, qw);
+        } else if constexpr (STAGES == 2) {
+            for (; t + 1 < nfull; t += 2) {
+                step(S0{}, Plain{}, t);
+                step(S1{}, Plain{}, t + 1);
             }
-        };
-        if (PINGPONG && lagging) key_loop(std::integral_constant<bool, PINGPONG>{});
-        else key_loop(std::integral_constant<bool, false>{});
+            for (; t < ntiles; ++t) {
+                if (t & 1) step(S1{}, Masked{}, t);
+                else step(S0{}, Masked{}, t);
+            }
+        } else {
+            for (; t + 2 < nfull; t += 3) {
+                step(S0{}, Plain{}, t);
+                step(S1{}, Plain{}, t + 1);
+                step(S2{}, Plain{}, t + 2);
+            }
+            for (; t < ntiles; ++t) {
+                const int r = t % 3;
+                if (r == 0) step(S0{}, Masked{}, t);
+                else if (r == 1) step(S1{}, Masked{}, t);
+                else step(S2{}, Masked{}, t);
+            }
+        }
 
         // Epilogue: O = acc / lb in BF16; rows >= sq fall outside the store bound.
         // Dividing by the sum of the rounded weights keeps them normalised, so
@@ -497,260 +607,7 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
         if constexpr (LSE) {
             if (half == 0 && row < a.sq) a.lse[int64_t(bh) * a.sq + row] = st.m * LN2 + logf(st.l);
         }
-        __syncthreads();   // LDS stages are reused by the next work item
-    };
-    for_each_item<CAUSAL>(tiles, total, process);
-}
-
-// ---------------------------------------------------------------------------
-// Two-group kernel: 4 waves x 64 query rows, one wave per SIMD (512 registers).
-// Each wave holds two 32-row groups, A = rows [qa, qa+32) and B = [qa+32,
-// qa+64), that share every K and V operand read from LDS (half the LDS
-// traffic per FLOP of the one-group kernel).  The key loop is software
-// pipelined so that one group's softmax VALU work sits beside the other
-// group's MFMAs in the same instruction stream:
-//   P1: load K(t); QK_A(t)            | softmax tail  B(t-1)
-//   P2: PV_B(t-1) (V(t-1) registers)  | softmax head  A(t)
-//   P3: QK_B(t) (K(t) registers)      | softmax tail  A(t)
-//   P4: load V(t); PV_A(t)            | softmax head  B(t)
-// Only tile t's LDS stage is read between barriers t and t+1, so two stages
-// suffice; the DMA of tile t+1 is issued right after barrier t.
-// ---------------------------------------------------------------------------
-template <int BN, bool MASKED, bool CAUSAL>
-__device__ __forceinline__ void load_k(const unsigned char* ks, const LdsOffsets& off, bf16x8 (&kr)[BN / 32][8],
-                                       int start, int sk, int qlast) {
-#pragma unroll
-    for (int kb = 0; kb < BN / 32; ++kb)
-        if (block_active<MASKED, CAUSAL>(start + kb * 32, sk, qlast)) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) kr[kb][c] = lds_read16(ks + kb * 32 * ROW_BYTES + off.k[c]);
-        }
-}
-
-template <int BN, bool MASKED, bool CAUSAL>
-__device__ __forceinline__ void qk_regs(const bf16x8 (&kr)[BN / 32][8], const bf16x8 (&qr)[8], f32x16 (&s)[BN / 32],
-                                        int start, int sk, int qw) {
-    const f32x16 zero = {};
-#pragma unroll
-    for (int kb = 0; kb < BN / 32; ++kb) {
-        s[kb] = zero;
-        if (block_active<MASKED, CAUSAL>(start + kb * 32, sk, qw)) {
-            s[kb] = mfma32(kr[kb][0], qr[0], zero);
-#pragma unroll
-            for (int c = 1; c < 8; ++c) s[kb] = mfma32(kr[kb][c], qr[c], s[kb]);
-        }
-    }
-}
-
-template <int BN, bool MASKED, bool CAUSAL>
-__device__ __forceinline__ void load_v(const unsigned char* vs, const LdsOffsets& off, bf16x8 (&vr)[BN / 32][2][4],
-                                       int start, int sk, int qlast) {
-#pragma unroll
-    for (int kb = 0; kb < BN / 32; ++kb)
-        if (block_active<MASKED, CAUSAL>(start + kb * 32, sk, qlast)) {
-#pragma unroll
-            for (int sub = 0; sub < 2; ++sub) {
-                const unsigned char* vb = vs + (kb * 32 + sub * 16) * ROW_BYTES;
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const bf16x4 lo = lds_read_tr(vb + off.v[0][db]);
-                    const bf16x4 hi = lds_read_tr(vb + off.v[1][db]);
-                    vr[kb][sub][db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                }
-            }
-        }
-}
-
-template <int BN, bool MASKED, bool CAUSAL>
-__device__ __forceinline__ void pv_regs(const bf16x8 (&vr)[BN / 32][2][4], const bf16x8 (&p)[BN / 32][2],
-                                        RowState& st, int start, int sk, int qw) {
-#pragma unroll
-    for (int kb = 0; kb < BN / 32; ++kb)
-        if (block_active<MASKED, CAUSAL>(start + kb * 32, sk, qw)) {
-#pragma unroll
-            for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-                for (int db = 0; db < 4; ++db) st.o[db] = mfma32(vr[kb][sub][db], p[kb][sub], st.o[db]);
-        }
-}
-
-template <int BN, bool CAUSAL, bool LSE>
-__global__ __launch_bounds__(256)
-void fwd_kernel_g2(Fav4Args a, int tiles, int total) {
-    constexpr int WAVES = 4, BM = 256, STAGES = 3;
-    constexpr int KB = BN / 32;
-    constexpr int TILE_BYTES = BN * ROW_BYTES;
-    constexpr int STAGE_BYTES = 2 * TILE_BYTES;          // K then V
-    constexpr int DMA = BN / 4 / WAVES;                  // 1 KiB DMA ops per wave per matrix
-    static_assert(BN % 32 == 0 && BN % (4 * WAVES) == 0, "tile shape");
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[STAGES * STAGE_BYTES];
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int col = lane & 31, half = lane >> 5;
-    const uint32_t row_bytes = uint32_t(a.heads) * ROW_BYTES;
-    const float scale2 = a.scale * LOG2E;
-    const uint32_t smem_base = lds_addr(smem);
-
-    LdsOffsets off;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) off.k[c] = col * ROW_BYTES + ((((2 * c) | half) ^ k_swz(col)) << 4);
-    {
-        const int r0 = half * 4 + ((lane & 15) >> 2);
-        const int gl = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int r = r0 + 8 * j;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-                off.v[j][db] = r * ROW_BYTES + (((db * 4 + gl) ^ v_swz(r)) << 4) + ((lane & 1) << 3);
-        }
-    }
-    uint32_t dk[DMA], dv[DMA];
-#pragma unroll
-    for (int i = 0; i < DMA; ++i) {
-        const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
-        dk[i] = r * row_bytes + ((p ^ k_swz(r)) << 4);
-        dv[i] = r * row_bytes + ((p ^ v_swz(r)) << 4);
-    }
-
-    auto process = [&](int bh, int tile) {
-        const int batch = bh / a.heads, head = bh - batch * a.heads;
-        const int q0 = tile * BM, qa = q0 + wave * 64, qb = qa + 32;
-        const int row_a = qa + col, row_b = qb + col;
-        const int64_t qrow0 = (int64_t(batch) * a.sq + q0) * a.heads + head;
-        const int64_t krow0 = int64_t(batch) * a.sk * a.heads + head;
-        const char* kbase = static_cast<const char*>(a.k) + krow0 * ROW_BYTES;
-        const char* vbase = static_cast<const char*>(a.v) + krow0 * ROW_BYTES;
-        const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + qrow0 * ROW_BYTES,
-                                    uint32_t(a.sq - q0 - 1) * row_bytes + ROW_BYTES);
-        const rsrc_t ro = make_rsrc(static_cast<char*>(a.o) + qrow0 * ROW_BYTES,
-                                    uint32_t(a.sq - q0 - 1) * row_bytes + ROW_BYTES);
-        const int kend = CAUSAL ? min(a.sk, q0 + BM) : a.sk;
-        const int ntiles = (kend + BN - 1) / BN;
-        const int nfull = (CAUSAL ? min(a.sk, q0 + 1) : a.sk) / BN;
-
-        // DMA of tile t into stage t % 3.  Tiles past the last are clamped to
-        // it, so the prefetch needs no branch (the copy lands in an idle stage).
-        auto issue = [&](int t) {
-            t = min(t, ntiles - 1);
-            const int64_t first = int64_t(t) * BN;
-            const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * row_bytes + ROW_BYTES;
-            const u32x4 rk = make_desc(kbase + first * row_bytes, bytes);
-            const u32x4 rv = make_desc(vbase + first * row_bytes, bytes);
-            const uint32_t ks = smem_base + (t % STAGES) * STAGE_BYTES + wave * DMA * 1024;
-#pragma unroll
-            for (int i = 0; i < DMA; ++i) {
-                dma16(rk, ks + i * 1024, dk[i]);
-                dma16(rv, ks + TILE_BYTES + i * 1024, dv[i]);
-            }
-        };
-
-        issue(0);
-        issue(1);
-        bf16x8 qra[8], qrb[8];
-        {
-            const uint32_t qoff = uint32_t(wave * 64 + col) * row_bytes + half * 16;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                qra[c] = load16(rq, qoff + c * 32);
-                qrb[c] = load16(rq, qoff + 32 * row_bytes + c * 32);
-            }
-            // Q lives in AGPRs (MFMA B operands may come from AGPRs on gfx950),
-            // leaving the 256 arch VGPRs to S, P and the K/V operands.
-#pragma unroll
-            for (int c = 0; c < 8; ++c) asm volatile("" : "+a"(qra[c]), "+a"(qrb[c]));
-        }
-        RowState sa, sb;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) sa.o[db] = sb.o[db] = f32x16{};
-        sa.m = sb.m = -__builtin_inff();
-        sa.lb = sb.lb = 0.f;
-        sa.l = sb.l = 0.f;
-        f32x16 s_a[KB], s_b[KB];
-        bf16x8 p_a[KB][2], p_b[KB][2];
-        bf16x8 kr[KB][8], vr[KB][2][4];
-        SmCarry ca, cb;
-
-        auto iter = [&](auto stage_c, auto masked_c, auto first_c, int t) {
-            constexpr int STAGE = decltype(stage_c)::value;
-            constexpr bool MASKED = decltype(masked_c)::value, FIRST = decltype(first_c)::value;
-            const unsigned char* ks = smem + STAGE * STAGE_BYTES;
-            const unsigned char* vs = ks + TILE_BYTES;
-            const int start = t * BN;
-            wait_vmem_keep<2 * DMA>();   // tile t landed; tile t+1 may still be in flight
-            __syncthreads();
-            issue(t + 2);
-            // P1: load K(t); QK_A(t) | softmax tail B(t-1)
-            load_k<BN, MASKED, CAUSAL>(ks, off, kr, start, a.sk, qb);
-            qk_regs<BN, MASKED, CAUSAL>(kr, qra, s_a, start, a.sk, qa);
-            if constexpr (!FIRST) softmax_tail<BN, LSE>(s_b, p_b, sb, cb, scale2);
-            // P2: PV_B(t-1) | softmax head A(t)
-            if constexpr (!FIRST) {
-                apply_rescale(sb, cb);
-                pv_regs<BN, MASKED, CAUSAL>(vr, p_b, sb, start - BN, a.sk, qb);
-            }
-            softmax_head<BN, MASKED, CAUSAL, LSE>(s_a, p_a, sa, ca, FIRST, start, a.sk, qa, row_a, half, scale2);
-            // P3: QK_B(t) | softmax tail A(t)
-            qk_regs<BN, MASKED, CAUSAL>(kr, qrb, s_b, start, a.sk, qb);
-            softmax_tail<BN, LSE>(s_a, p_a, sa, ca, scale2);
-            // P4: load V(t); PV_A(t) | softmax head B(t)
-            apply_rescale(sa, ca);
-            load_v<BN, MASKED, CAUSAL>(vs, off, vr, start, a.sk, qb);
-            pv_regs<BN, MASKED, CAUSAL>(vr, p_a, sa, start, a.sk, qa);
-            softmax_head<BN, MASKED, CAUSAL, LSE>(s_b, p_b, sb, cb, FIRST, start, a.sk, qb, row_b, half, scale2);
-        };
-        using S0 = std::integral_constant<int, 0>;
-        using S1 = std::integral_constant<int, 1>;
-        using S2 = std::integral_constant<int, 2>;
-        using Plain = std::integral_constant<bool, false>;
-        using Masked = std::integral_constant<bool, true>;
-        using First = std::integral_constant<bool, true>;
-        using Later = std::integral_constant<bool, false>;
-        if (nfull > 0) iter(S0{}, Plain{}, First{}, 0);
-        else iter(S0{}, Masked{}, First{}, 0);
-        int t = 1;
-        for (; t + 2 < nfull; t += 3) {
-            iter(S1{}, Plain{}, Later{}, t);
-            iter(S2{}, Plain{}, Later{}, t + 1);
-            iter(S0{}, Plain{}, Later{}, t + 2);
-        }
-        for (; t < ntiles; ++t) {
-            // The masked body is correct for the (at most two) plain tiles left too.
-            const int r = t % 3;
-            if (r == 0) iter(S0{}, Masked{}, Later{}, t);
-            else if (r == 1) iter(S1{}, Masked{}, Later{}, t);
-            else iter(S2{}, Masked{}, Later{}, t);
-        }
-        // Drain: group B still owes softmax tail + PV of the last tile.
-        softmax_tail<BN, LSE>(s_b, p_b, sb, cb, scale2);
-        apply_rescale(sb, cb);
-        pv_regs<BN, true, CAUSAL>(vr, p_b, sb, (ntiles - 1) * BN, a.sk, qb);
-
-        // Epilogue (both groups): O = acc / lb in BF16, LSE = m*ln2 + ln(l).
-        const uint32_t obase = uint32_t(wave * 64 + col) * row_bytes + half * 8;
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            const RowState& st = g ? sb : sa;
-            const float inv = 1.f / st.lb;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-#pragma unroll
-                for (int vg = 0; vg < 4; ++vg) {
-                    const f32x2 x0 = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv};
-                    const f32x2 x1 = {st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
-                    const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
-                    const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
-                    store8(ro, obase + g * 32 * row_bytes + (db * 32 + vg * 8) * 2,
-                           bf16x4{y0[0], y0[1], y1[0], y1[1]});
-                }
-            }
-            if constexpr (LSE) {
-                const int row = g ? row_b : row_a;
-                if (half == 0 && row < a.sq) a.lse[int64_t(bh) * a.sq + row] = st.m * LN2 + logf(st.l);
-            }
-        }
-        wait_vmem();       // the clamped prefetches have landed before the stages are reused
+        wait_vmem();       // clamped prefetches have landed before the stages are reused
         __syncthreads();
     };
     for_each_item<CAUSAL>(tiles, total, process);
