@@ -164,46 +164,6 @@ __device__ __forceinline__ void exp_unit(const f32x16& s, int sub, bf16x8& p, Sm
     p = bf16x8{b0[0], b0[1], b1[0], b1[1], b2[0], b2[1], b3[0], b3[1]};
 }
 
-// Softmax head: masks, row max, conditional base update (log2 units), and P
-// of the first half of the tile's 16-key units.  The O rescale it decides is
-// applied by apply_rescale before the tile's PV product.
-template <int BN, bool MASKED, bool CAUSAL, bool LSE>
-__device__ __forceinline__ void softmax_head(f32x16 (&s)[BN / 32], bf16x8 (&p)[BN / 32][2], RowState& st,
-                                             SmCarry& c, bool first, int start, int sk, int qw, int row,
-                                             int half, float scale2) {
-    constexpr int KB = BN / 32;
-    tile_mask<BN, MASKED, CAUSAL>(s, start, sk, qw, row, half);
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
-    mx = xhalf_max(mx);
-    const float cand = fmaxf(st.m, mx * scale2);
-    const bool update = first || cand > st.m + RESCALE_THRESHOLD;
-    const float next = update ? cand : st.m;
-    c.alpha = exp2_native(st.m - next);   // 0 on the first tile, 1 if no update
-    c.rescale = !first && __builtin_amdgcn_ballot_w64(update) != 0;
-    st.m = next;
-    c.neg = -next;
-    c.pb0 = c.pb1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) c.part[i] = 0.f;
-#pragma unroll
-    for (int u = 0; u < KB; ++u) exp_unit<LSE>(s[u >> 1], u & 1, p[u >> 1][u & 1], c, scale2);
-}
-
-// Softmax tail: P of the remaining units, running sums.
-template <int BN, bool LSE>
-__device__ __forceinline__ void softmax_tail(const f32x16 (&s)[BN / 32], bf16x8 (&p)[BN / 32][2], RowState& st,
-                                             SmCarry& c, float scale2) {
-    constexpr int KB = BN / 32;
-#pragma unroll
-    for (int u = KB; u < 2 * KB; ++u) exp_unit<LSE>(s[u >> 1], u & 1, p[u >> 1][u & 1], c, scale2);
-    st.lb = st.lb * c.alpha + xhalf_sum(c.pb0 + c.pb1);
-    if constexpr (LSE) st.l = st.l * c.alpha + xhalf_sum((c.part[0] + c.part[1]) + (c.part[2] + c.part[3]));
-}
-
 // One 16-register accumulator block at a time, fenced, so the (AGPR-resident)
 // accumulators need at most 16 VGPR temporaries while being scaled.
 __device__ __forceinline__ void apply_rescale(RowState& st, const SmCarry& c) {
@@ -216,68 +176,32 @@ __device__ __forceinline__ void apply_rescale(RowState& st, const SmCarry& c) {
     }
 }
 
-// Whole-tile softmax (single-group kernel).
-template <int BN, bool MASKED, bool CAUSAL, bool LSE>
-__device__ __forceinline__ void tile_softmax(f32x16 (&s)[BN / 32], bf16x8 (&p)[BN / 32][2], RowState& st,
-                                             bool first, int start, int sk, int qw, int row, int half,
-                                             float scale2) {
-    SmCarry c;
-    softmax_head<BN, MASKED, CAUSAL, LSE>(s, p, st, c, first, start, sk, qw, row, half, scale2);
-    apply_rescale(st, c);
-    softmax_tail<BN, LSE>(s, p, st, c, scale2);
+// Row max of one tile's raw logits, combined over the two lane halves.
+template <int BN>
+__device__ __forceinline__ float tile_rowmax(const f32x16 (&s)[BN / 32]) {
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
+    return xhalf_max(mx);
 }
 
-// O^T += V^T.P^T for one tile (S element v of lane half h is MFMA k = h*8 + v%8).
-template <int BN, bool MASKED, bool CAUSAL>
-__device__ __forceinline__ void tile_pv(const unsigned char* vs, const LdsOffsets& off,
-                                        const bf16x8 (&p)[BN / 32][2], RowState& st, int start, int sk,
-                                        int qw) {
-    constexpr int KB = BN / 32;
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-        if (!block_active<MASKED, CAUSAL>(start + kb * 32, sk, qw)) continue;
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            const unsigned char* vb = vs + (kb * 32 + sub * 16) * ROW_BYTES;
-            bf16x8 vop[4];
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const bf16x4 lo = lds_read_tr(vb + off.v[0][db]);
-                const bf16x4 hi = lds_read_tr(vb + off.v[1][db]);
-                vop[db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            }
-#pragma unroll
-            for (int db = 0; db < 4; ++db) st.o[db] = mfma32(vop[db], p[kb][sub], st.o[db]);
-        }
-    }
-}
-
-// One key tile for one 32-row wave, software pipelined inside the tile:
-//   QK block 0 | QK block 1 (+ mask/max of block 0) | base update
-//   exp(unit 0) | [rescale O] | PV(unit u-1) beside exp(unit u) ... | PV(last)
+// Softmax and PV of one key tile whose scores S^T are already in `s`, for one
+// 32-row wave, software pipelined inside the tile:
+//   masks, row max, base update | exp(unit 0) | [rescale O] |
+//   PV(unit u-1) beside exp(unit u) ... | PV(last)
 // A unit is 16 keys (one PV k-step for all four 32-dim blocks).  Keeping the
 // rare O-rescale branch in front of the first PV leaves the exp/PV overlap in
 // one basic block, where the scheduler can interleave the VALU work of unit u
 // with the MFMAs of unit u-1.
 template <int BN, bool MASKED, bool CAUSAL, bool LSE>
-__device__ __forceinline__ void attend_fused(const unsigned char* ks, const unsigned char* vs, const LdsOffsets& off,
-                                             const bf16x8 (&qr)[8], RowState& st, bool first, int start, int sk,
-                                             int qw, int row, int half, float scale2) {
+__device__ __forceinline__ void attend_tail(f32x16 (&s)[BN / 32], const unsigned char* vs, const LdsOffsets& off,
+                                            RowState& st, bool first, int start, int sk, int qw, int row, int half,
+                                            float scale2) {
     constexpr int KB = BN / 32, U = 2 * KB;
-    f32x16 s[KB];
-    // Raised issue priority while this wave feeds QK^T MFMAs: when the two
-    // waves of a SIMD compete, the one in its MFMA phase goes first and the
-    // other fills the VALU slots (measured +5% at B32H8S4096).
-    __builtin_amdgcn_s_setprio(1);
-    tile_qk<BN, MASKED, CAUSAL>(ks, off, qr, s, start, sk, qw);
-    __builtin_amdgcn_s_setprio(0);
     tile_mask<BN, MASKED, CAUSAL>(s, start, sk, qw, row, half);
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
-    mx = xhalf_max(mx);
+    const float mx = tile_rowmax<BN>(s);
     const float cand = fmaxf(st.m, mx * scale2);
     const bool update = first || cand > st.m + RESCALE_THRESHOLD;
     const float next = update ? cand : st.m;
@@ -314,15 +238,18 @@ __device__ __forceinline__ void attend_fused(const unsigned char* ks, const unsi
     if constexpr (LSE) st.l = st.l * c.alpha + xhalf_sum((c.part[0] + c.part[1]) + (c.part[2] + c.part[3]));
 }
 
-// Row max of one tile's raw logits, combined over the two lane halves.
-template <int BN>
-__device__ __forceinline__ float tile_rowmax(const f32x16 (&s)[BN / 32]) {
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int kb = 0; kb < BN / 32; ++kb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
-    return xhalf_max(mx);
+// QK^T of one tile at raised issue priority, then attend_tail.  When the two
+// waves of a SIMD compete, the one feeding QK^T MFMAs goes first and the
+// other fills the VALU slots (measured +5% at B32H8S4096).
+template <int BN, bool MASKED, bool CAUSAL, bool LSE>
+__device__ __forceinline__ void attend_fused(const unsigned char* ks, const unsigned char* vs, const LdsOffsets& off,
+                                             const bf16x8 (&qr)[8], RowState& st, bool first, int start, int sk,
+                                             int qw, int row, int half, float scale2) {
+    f32x16 s[BN / 32];
+    __builtin_amdgcn_s_setprio(1);
+    tile_qk<BN, MASKED, CAUSAL>(ks, off, qr, s, start, sk, qw);
+    __builtin_amdgcn_s_setprio(0);
+    attend_tail<BN, MASKED, CAUSAL, LSE>(s, vs, off, st, first, start, sk, qw, row, half, scale2);
 }
 
 // Base update from a precomputed row max, then all of the tile's P units and
