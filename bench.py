@@ -16,6 +16,13 @@ reference's sampled rows (bshd.py:147-148) for a subset of (b, h) pairs.
 
 The ``cpu_baseline`` leg times the FP64 oracle on this host's cores on a
 bounded sample of (b, h) slices of the same dense workload (a baseline only).
+
+The ``comparator`` leg times torch's scaled_dot_product_attention on the same
+device and inputs (contiguous BHSD copies, its fused flash backend, else its
+memory-efficient one; never the unfused math path), interleaved with this
+library's kernel in A-B-B-A order, and reports the speedup and the largest
+difference between the two outputs.  ``provenance`` records what was measured:
+library and source hashes, toolchain and torch versions, device and clocks.
 """
 from __future__ import annotations
 
@@ -53,6 +60,7 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     p.add_argument("--sweep", default="", help="comma list of extra sequence lengths to time (report only)")
+    p.add_argument("--no-comparator", action="store_true", help="skip the torch SDPA comparator")
     p.add_argument("--pmc-pass", action="store_true",
                    help="profiling mode for counter runs: two eager launches per mask type, then a "
                         "plain 1 GiB device copy (HBM counter calibration); prints no JSON")
@@ -158,6 +166,136 @@ def cpu_baseline(torch, orc, q, k, v, budget_s):
                        f"{elapsed * len(pairs) / done:.1f} s")
 
 
+def time_eager(torch, fn, steps, warmup, stream):
+    """Per-launch microseconds of `steps` eager launches between events on `stream`."""
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) * 1000.0 / steps
+
+
+def comparator(torch, orc, runner, q, k, v, o, stream, args, causal_list):
+    """torch SDPA (fused backends only) vs this library on the same inputs, A-B-B-A."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    b, s, h, d = q.shape
+    qh, kh, vh = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    scale = 1.0 / math.sqrt(d)
+    backend = None
+    for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel([be]):
+                F.scaled_dot_product_attention(qh[:1, :1, :256], kh[:1, :1, :256], vh[:1, :1, :256], scale=scale)
+            torch.cuda.synchronize()
+            backend = (name, be)
+            break
+        except RuntimeError:
+            continue
+    if backend is None:
+        return None
+    out = {"name": f"torch.nn.functional.scaled_dot_product_attention, {backend[0]} backend "
+                   f"(torch {torch.__version__})",
+           "layout": "contiguous BHSD copies of the same Q/K/V (its preferred layout; copies not timed)"}
+    for causal in causal_list:
+        ref = [None]
+
+        def theirs():
+            with sdpa_kernel([backend[1]]):
+                ref[0] = F.scaled_dot_product_attention(qh, kh, vh, is_causal=causal, scale=scale)
+
+        ours = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
+        t = {"ours": [], "theirs": []}
+        for who in ("ours", "theirs", "theirs", "ours"):
+            t[who].append(time_eager(torch, ours if who == "ours" else theirs, args.steps, args.warmup, stream))
+        torch.cuda.synchronize()
+        diff = (ref[0].transpose(1, 2).float() - o.float()).abs().max().item()
+        flop = orc.flops(b, h, s, s, causal)
+        us_o, us_t = statistics.mean(t["ours"]), statistics.mean(t["theirs"])
+        out["causal" if causal else "dense"] = dict(
+            tflops=round(flop / us_t / 1e6, 2), us_per_launch=round(us_t, 3),
+            ours_tflops_eager=round(flop / us_o / 1e6, 2), speedup=round(us_t / us_o, 4),
+            max_abs_diff_vs_ours=round(diff, 5))
+        print(f"# comparator causal={causal}: SDPA {flop / us_t / 1e6:.1f} TFLOP/s, ours {flop / us_o / 1e6:.1f} "
+              f"(eager, ABBA), speedup {us_t / us_o:.3f}, max|diff| {diff:.4f}", file=sys.stderr, flush=True)
+    del qh, kh, vh
+    return out
+
+
+def _run(cmd, timeout=20):
+    import subprocess
+    try:
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+        return r.stdout if r.returncode == 0 else None
+    except (OSError, subprocess.SubprocessError):
+        return None
+
+
+def gpu_clocks():
+    """Current clocks in MHz per domain ({"GFX_0": 2398, ..., "MEM_0": 2000}) from amd-smi, or None."""
+    txt = _run(["amd-smi", "metric", "-c"])
+    if not txt:
+        return None
+    clocks, domain = {}, None
+    for ln in txt.splitlines():
+        t = ln.strip()
+        if t.endswith(":") and " " not in t:
+            domain = t[:-1]
+        elif t.startswith("CLK:") and domain and t.endswith("MHz"):
+            try:
+                clocks[domain] = int(float(t.split()[1]))
+            except ValueError:
+                pass
+    return {d: c for d, c in clocks.items() if d.startswith(("GFX", "MEM"))} or None
+
+
+def loaded_gfx_clock(torch, fn, stream, launches=200, reps=4):
+    """Mean GFX clock (MHz) read by amd-smi while a graph of `launches` x fn is replayed back to back."""
+    import threading
+    with torch.cuda.stream(stream):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(launches):
+                fn()
+    got = {}
+    reader = threading.Thread(target=lambda: (time.sleep(0.3), got.update(c=gpu_clocks())))
+    with torch.cuda.stream(stream):
+        g.replay()
+        reader.start()
+        for _ in range(reps - 1):
+            g.replay()
+    torch.cuda.synchronize()
+    reader.join()
+    del g
+    gfx = [v for d, v in (got.get("c") or {}).items() if d.startswith("GFX")]
+    return round(statistics.mean(gfx)) if gfx else None
+
+
+def provenance(torch, lib_path):
+    import hashlib
+    h = lambda p: hashlib.sha256(Path(p).read_bytes()).hexdigest()
+    src = ROOT / "flash-attention-v4-rocm_amd" / "csrc"
+    srcs = sorted(src.glob("*")) + [ROOT / "include" / "fav4_bshd.h"]
+    digest = hashlib.sha256()
+    for p in srcs:
+        digest.update(p.name.encode())
+        digest.update(p.read_bytes())
+    hipcc = _run(["hipcc", "--version"])
+    prop = torch.cuda.get_device_properties(0)
+    return {"library": str(Path(lib_path).relative_to(ROOT)), "library_sha256": h(lib_path),
+            "sources_sha256": digest.hexdigest(),
+            "hipcc": next((ln for ln in (hipcc or "").splitlines() if "HIP version" in ln), None),
+            "torch": torch.__version__, "device": f"{prop.name} {prop.gcnArchName} {prop.multi_processor_count} CUs",
+            "clocks_before": gpu_clocks()}
+
+
 def read_traffic():
     if not TRAFFIC_FILE.exists():
         return None
@@ -183,6 +321,7 @@ def main():
         return
 
     b, h, s = args.batch, args.heads, args.seq
+    prov = provenance(torch, pkg.LIB_PATH)
     q, k, v = make_inputs(torch, b, h, s)
     o = torch.empty_like(q)
     stream = torch.cuda.Stream()
@@ -208,6 +347,10 @@ def main():
               f"({flop / us / 1e6 / PEAK_BF16_TFLOPS * 100:.1f}% of peak) check={check}",
               file=sys.stderr, flush=True)
 
+    cmp = None
+    if not args.no_comparator:
+        cmp = comparator(torch, orc, runner, q, k, v, o, stream, args, list(results))
+
     sweep = {}
     for n in [int(x) for x in args.sweep.split(",") if x]:
         del q, k, v, o
@@ -223,12 +366,18 @@ def main():
             print(f"# sweep S{n} causal={causal}: {us:.1f} us, {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)
 
     dense = results[False]
+    clk = loaded_gfx_clock(torch, lambda: runner.call(q, k, v, o, None, False, args.config,
+                                                      stream=stream.cuda_stream), stream)
     traffic = read_traffic()
     compulsory = 2 * b * h * 128 * (2 * s + 2 * s)
     roofline = dict(bound="mfma", achieved=round(dense["tflops"], 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
                     frac=round(dense["tflops"] / PEAK_BF16_TFLOPS, 4), traffic=traffic,
                     kernel="fav4::fwd_kernel (dense)", flop_per_launch=dense["flop"],
-                    avg_launch_us=round(dense["us"], 3), compulsory_hbm_bytes=compulsory)
+                    avg_launch_us=round(dense["us"], 3), compulsory_hbm_bytes=compulsory,
+                    hbm_roofline_tflops=round(dense["flop"] / compulsory * HBM_TBPS, 1),
+                    gfx_clock_mhz_under_load=clk,
+                    peak_at_loaded_clock=round(PEAK_BF16_TFLOPS * clk / 2400, 1) if clk else None,
+                    frac_at_loaded_clock=round(dense["tflops"] / (PEAK_BF16_TFLOPS * clk / 2400), 4) if clk else None)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(torch, orc, q, k, v, args.cpu_seconds) if not sweep else None
@@ -258,6 +407,9 @@ def main():
                               frac_of_peak=round(c["tflops"] / PEAK_BF16_TFLOPS, 4),
                               samples_us=[round(x, 2) for x in c["samples_us"]])
     line["dense_samples_us"] = [round(x, 2) for x in dense["samples_us"]]
+    line["comparator"] = cmp
+    prov["clocks_after"] = gpu_clocks()
+    line["provenance"] = prov
     if sweep:
         line["sweep"] = sweep
     print(json.dumps(line), flush=True)
