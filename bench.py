@@ -61,6 +61,7 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     p.add_argument("--sweep", default="", help="comma list of extra sequence lengths to time (report only)")
     p.add_argument("--no-comparator", action="store_true", help="skip the torch SDPA comparator")
+    p.add_argument("--no-splitkv", action="store_true", help="skip the split-KV report (B1 H8 Sq1024 Sk32768)")
     p.add_argument("--pmc-pass", action="store_true",
                    help="profiling mode for counter runs: two eager launches per mask type, then a "
                         "plain 1 GiB device copy (HBM counter calibration); prints no JSON")
@@ -229,6 +230,45 @@ def comparator(torch, orc, runner, q, k, v, o, stream, args, causal_list):
     return out
 
 
+def splitkv_report(torch, orc, runner, args, stream, b=1, h=8, sq=1024, sk=32768):
+    """Few (b, h, q tile) items and long keys: the single-pass forward against the
+    split-KV forward (Auto chunk count), both graph-timed, each output checked on
+    sampled rows first."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11939)
+    mk = lambda s: torch.randn((b, s, h, 128), device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
+    q, k, v = mk(sq), mk(sk), mk(sk)
+    o = torch.empty_like(q)
+    out = {"workload": f"B{b} H{h} Sq={sq} Sk={sk} D128 BF16, LSE off"}
+    for causal in (False, True):
+        splits = runner.splitkv_select(b, h, sq, sk, causal)
+        ws = torch.empty(max(runner.splitkv_workspace_size(b, h, sq, sk, causal, 0), 1), device="cuda",
+                         dtype=torch.uint8)
+        plain = lambda: runner.call(q, k, v, o, None, causal, 0, stream=stream.cuda_stream)
+        split = lambda: runner.call_splitkv(q, k, v, o, None, causal, 0, workspace=ws, stream=stream.cuda_stream)
+        flop = orc.flops(b, h, sq, sk, causal)
+        res = {"splits": splits, "workspace_bytes": ws.numel()}
+        for name, fn in (("plain", plain), ("splitkv", split)):
+            o.fill_(float("nan"))
+            with torch.cuda.stream(stream):
+                fn()
+            torch.cuda.synchronize()
+            err, _ = check_rows(torch, orc, q, k, v, o, causal, [(0, 0), (0, h - 1)])
+            if not orc.check_north_star_tolerance(err):
+                raise SystemExit(f"split-KV report: {name} check failed (causal={causal}): {err}")
+            us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream))
+            res[name] = dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1))
+        res["speedup"] = round(res["plain"]["us"] / res["splitkv"]["us"], 2)
+        out["causal" if causal else "dense"] = res
+        print(f"# splitkv B{b} H{h} {sq}x{sk} causal={causal}: plain {res['plain']['tflops']} TFLOP/s, "
+              f"split-KV ({splits} chunks) {res['splitkv']['tflops']} TFLOP/s, x{res['speedup']}",
+              file=sys.stderr, flush=True)
+        del ws
+    del q, k, v, o
+    torch.cuda.empty_cache()
+    return out
+
+
 def _run(cmd, timeout=20):
     import subprocess
     try:
@@ -350,6 +390,7 @@ def main():
     cmp = None
     if not args.no_comparator:
         cmp = comparator(torch, orc, runner, q, k, v, o, stream, args, list(results))
+    skv = None if args.no_splitkv else splitkv_report(torch, orc, runner, args, stream)
 
     sweep = {}
     for n in [int(x) for x in args.sweep.split(",") if x]:
@@ -408,6 +449,7 @@ def main():
                               samples_us=[round(x, 2) for x in c["samples_us"]])
     line["dense_samples_us"] = [round(x, 2) for x in dense["samples_us"]]
     line["comparator"] = cmp
+    line["splitkv"] = skv
     prov["clocks_after"] = gpu_clocks()
     line["provenance"] = prov
     if sweep:

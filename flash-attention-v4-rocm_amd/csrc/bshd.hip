@@ -6,6 +6,7 @@
 #include "fav4_bshd.h"
 #include "bshd_kernel.hpp"
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstdint>
@@ -41,6 +42,96 @@ int dispatch(const Fav4Args& a, int config, hipStream_t stream) {
     }
 }
 
+// Argument checks of src/bshd.hip:27-34, in the same order, before any HIP call.
+int validate(const Fav4Args* a, int causal, int config) {
+    if (!a || !a->q || !a->k || !a->v || !a->o || a->batch <= 0 || a->heads <= 0 || a->sq <= 0 ||
+        a->sk <= 0 || (causal != 0 && causal != 1) || config < 0 || config > 3 ||
+        !std::isfinite(a->scale) || a->scale <= 0)
+        return hipErrorInvalidValue;
+    if (a->batch > INT_MAX / a->heads || a->heads > INT_MAX / 128 ||
+        a->sq > INT_MAX / (a->heads * 128) || a->sk > INT_MAX / (a->heads * 128) ||
+        ((reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->k) |
+          reinterpret_cast<uintptr_t>(a->v) | reinterpret_cast<uintptr_t>(a->o)) & 15))
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+// ---- split-KV -------------------------------------------------------------
+constexpr int SPLIT_BM = 256, SPLIT_BN = 64;
+constexpr int MAX_SPLITS = 256;          // accepted explicit split counts
+constexpr int AUTO_MAX_SPLITS = 64;      // Auto never goes beyond this
+constexpr int MIN_TILES_PER_SPLIT = 4;   // Auto keeps >= 256 keys per chunk
+constexpr int MAX_SPLIT_SQ = 1 << 22;    // keeps a chunk's O rows under a 4 GiB buffer bound
+
+struct SplitPlan {
+    int splits, tps;   // chunks and key tiles per chunk
+};
+
+int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    return cus;
+}
+
+// Chunking of the key range a row can see (top-left causal never shows a key
+// past sq - 1); `req` = 0 picks enough chunks for about two workgroups per CU.
+// The count is then rounded so that no chunk starts past that range.
+SplitPlan split_plan(const Fav4Args& a, int causal, int req) {
+    const int tiles = (a.sq + SPLIT_BM - 1) / SPLIT_BM;
+    const int keys = causal ? std::min(a.sk, a.sq) : a.sk;
+    const int ktiles = (keys + SPLIT_BN - 1) / SPLIT_BN;
+    int64_t splits = req;
+    if (splits == 0) {
+        const int64_t items = int64_t(a.batch) * a.heads * tiles;
+        splits = (2 * int64_t(device_cus()) + items - 1) / items;
+        splits = std::min<int64_t>(splits, std::min(AUTO_MAX_SPLITS, std::max(1, ktiles / MIN_TILES_PER_SPLIT)));
+    }
+    splits = std::max<int64_t>(1, std::min<int64_t>(splits, ktiles));
+    const int tps = int((ktiles + splits - 1) / splits);
+    return {(ktiles + tps - 1) / tps, tps};
+}
+
+int64_t split_workspace(const Fav4Args& a, const SplitPlan& p) {
+    if (p.splits <= 1) return 0;
+    return int64_t(p.splits) * a.batch * a.heads * a.sq * (fav4::D * 4 + 2 * 4);
+}
+
+// Shape-only checks for the split-KV queries (no buffers needed yet).
+int split_shape_ok(const Fav4Args* a, int causal, int splits) {
+    if (!a || a->batch <= 0 || a->heads <= 0 || a->sq <= 0 || a->sk <= 0 || (causal != 0 && causal != 1) ||
+        a->batch > INT_MAX / a->heads || a->heads > INT_MAX / 128 || a->sq > INT_MAX / (a->heads * 128) ||
+        a->sk > INT_MAX / (a->heads * 128) || splits < 0 || splits > MAX_SPLITS || a->sq > MAX_SPLIT_SQ)
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+int split_args_ok(const Fav4Args* a, int causal, int splits) {
+    const int st = validate(a, causal, 0);
+    return st != hipSuccess ? st : split_shape_ok(a, causal, splits);
+}
+
+template <bool CAUSAL>
+int launch_split(const Fav4Args& a, const SplitPlan& p, void* ws, hipStream_t stream) {
+    const int tiles = (a.sq + SPLIT_BM - 1) / SPLIT_BM;
+    const int64_t total = int64_t(a.batch) * a.heads * tiles * p.splits;
+    const int64_t rows = int64_t(a.batch) * a.heads * a.sq;
+    if (total > INT_MAX || (rows + 7) / 8 > INT_MAX) return hipErrorInvalidValue;
+    fav4::SplitArgs sp;
+    sp.o_part = static_cast<float*>(ws);
+    sp.lse_part = sp.o_part + int64_t(p.splits) * rows * fav4::D;
+    sp.splits = p.splits;
+    sp.tps = p.tps;
+    const int grid = int(total < MAX_GRID ? total : MAX_GRID);
+    hipLaunchKernelGGL((fav4::fwd_kernel_split<SPLIT_BN, CAUSAL>), dim3(grid), dim3(512), 0, stream, a, sp, tiles,
+                       int(total));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(fav4::combine_kernel, dim3(unsigned((rows + 7) / 8)), dim3(256), 0, stream, a, sp);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 // Replaces src/bshd.hip:23-25.  Small query lengths use 128-row workgroups so
@@ -53,15 +144,34 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_select_config(co
 // Replaces src/bshd.hip:26-38.
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward(const Fav4Args* a, int causal, int config,
                                                                 hipStream_t stream) {
-    if (!a || !a->q || !a->k || !a->v || !a->o || a->batch <= 0 || a->heads <= 0 || a->sq <= 0 ||
-        a->sk <= 0 || (causal != 0 && causal != 1) || config < 0 || config > 3 ||
-        !std::isfinite(a->scale) || a->scale <= 0)
-        return hipErrorInvalidValue;
-    if (a->batch > INT_MAX / a->heads || a->heads > INT_MAX / 128 ||
-        a->sq > INT_MAX / (a->heads * 128) || a->sk > INT_MAX / (a->heads * 128) ||
-        ((reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->k) |
-          reinterpret_cast<uintptr_t>(a->v) | reinterpret_cast<uintptr_t>(a->o)) & 15))
-        return hipErrorInvalidValue;
+    const int st = validate(a, causal, config);
+    if (st != hipSuccess) return st;
     if (config == 0) config = fav4_bshd_select_config(a);
     return causal ? dispatch<true>(*a, config, stream) : dispatch<false>(*a, config, stream);
+}
+
+// Split-KV entry points (no counterpart in the reference; see the header).
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_splitkv_select(const Fav4Args* a, int causal) {
+    if (split_shape_ok(a, causal, 0) != hipSuccess) return -1;
+    return split_plan(*a, causal, 0).splits;
+}
+
+extern "C" __attribute__((visibility("default"))) long long fav4_bshd_splitkv_workspace_size(const Fav4Args* a,
+                                                                                          int causal, int splits) {
+    if (split_shape_ok(a, causal, splits) != hipSuccess) return -1;
+    return split_workspace(*a, split_plan(*a, causal, splits));
+}
+
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv(const Fav4Args* a, int causal,
+                                                                        int splits, void* workspace,
+                                                                        size_t workspace_bytes,
+                                                                        hipStream_t stream) {
+    const int st = split_args_ok(a, causal, splits);
+    if (st != hipSuccess) return st;
+    const SplitPlan p = split_plan(*a, causal, splits);
+    if (p.splits == 1) return fav4_bshd_forward(a, causal, 0, stream);
+    const int64_t need = split_workspace(*a, p);
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || uint64_t(need) > workspace_bytes)
+        return hipErrorInvalidValue;
+    return causal ? launch_split<true>(*a, p, workspace, stream) : launch_split<false>(*a, p, workspace, stream);
 }

@@ -195,7 +195,10 @@ __device__ __forceinline__ float tile_rowmax(const f32x16 (&s)[BN / 32]) {
 // rare O-rescale branch in front of the first PV leaves the exp/PV overlap in
 // one basic block, where the scheduler can interleave the VALU work of unit u
 // with the MFMAs of unit u-1.
-template <int BN, bool MASKED, bool CAUSAL, bool LSE>
+// EMPTY: some rows may have seen no visible key yet (a split-KV key chunk
+// past a causal row's diagonal).  Their base stays -inf and the weights are
+// computed against 0 instead, so they come out 0 rather than NaN.
+template <int BN, bool MASKED, bool CAUSAL, bool LSE, bool EMPTY = false>
 __device__ __forceinline__ void attend_tail(f32x16 (&s)[BN / 32], const unsigned char* vs, const LdsOffsets& off,
                                             RowState& st, bool first, int start, int sk, int qw, int row, int half,
                                             float scale2) {
@@ -205,11 +208,13 @@ __device__ __forceinline__ void attend_tail(f32x16 (&s)[BN / 32], const unsigned
     const float cand = fmaxf(st.m, mx * scale2);
     const bool update = first || cand > st.m + RESCALE_THRESHOLD;
     const float next = update ? cand : st.m;
+    float base = next;
+    if constexpr (EMPTY && MASKED) base = next == -__builtin_inff() ? 0.f : next;
     SmCarry c;
-    c.alpha = exp2_native(st.m - next);
+    c.alpha = exp2_native(st.m - base);
     c.rescale = !first && __builtin_amdgcn_ballot_w64(update) != 0;
     st.m = next;
-    c.neg = -next;
+    c.neg = -base;
     c.pb0 = c.pb1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) c.part[i] = 0.f;
@@ -241,7 +246,7 @@ __device__ __forceinline__ void attend_tail(f32x16 (&s)[BN / 32], const unsigned
 // QK^T of one tile at raised issue priority, then attend_tail.  When the two
 // waves of a SIMD compete, the one feeding QK^T MFMAs goes first and the
 // other fills the VALU slots (measured +5% at B32H8S4096).
-template <int BN, bool MASKED, bool CAUSAL, bool LSE>
+template <int BN, bool MASKED, bool CAUSAL, bool LSE, bool EMPTY = false>
 __device__ __forceinline__ void attend_fused(const unsigned char* ks, const unsigned char* vs, const LdsOffsets& off,
                                              const bf16x8 (&qr)[8], RowState& st, bool first, int start, int sk,
                                              int qw, int row, int half, float scale2) {
@@ -249,7 +254,7 @@ __device__ __forceinline__ void attend_fused(const unsigned char* ks, const unsi
     __builtin_amdgcn_s_setprio(1);
     tile_qk<BN, MASKED, CAUSAL>(ks, off, qr, s, start, sk, qw);
     __builtin_amdgcn_s_setprio(0);
-    attend_tail<BN, MASKED, CAUSAL, LSE>(s, vs, off, st, first, start, sk, qw, row, half, scale2);
+    attend_tail<BN, MASKED, CAUSAL, LSE, EMPTY>(s, vs, off, st, first, start, sk, qw, row, half, scale2);
 }
 
 // Base update from a precomputed row max, then all of the tile's P units and
@@ -538,6 +543,209 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
         __syncthreads();
     };
     for_each_item<CAUSAL>(tiles, total, process);
+}
+
+// ---------------------------------------------------------------------------
+// Split-KV: the key range of every (batch, head, 256-row q tile) is cut into
+// `splits` chunks of `tps` key tiles, each chunk is attended by its own
+// workgroup (same tile body as fwd_kernel<8, BN, ..., 2 stages>), and a
+// second kernel merges the chunks.  For few (b, h, q tile) items and long
+// keys this fills the GPU where one workgroup per item cannot.
+// Workspace (FP32, caller-owned):
+//   o_part  [splits][B*H][sq][128]  O of the chunk, normalised by its own
+//                                    BF16 weight sum lb_s
+//   lse_part[splits][B*H][sq][2]    log2-domain sums of the chunk:
+//                                    (m_s + log2 lb_s, m_s + log2 l_s)
+// The merge weights chunk s by 2^(m_s) lb_s (the first log-sum), which makes
+// the merged O exactly the single-pass acc / lb; the LSE output is
+// ln 2 * log2(sum_s 2^(m_s) l_s) from the second, the single-pass FP32 sum.
+// Rows with no visible key in a chunk (causal) carry -inf and weight 0.
+// ---------------------------------------------------------------------------
+struct SplitArgs {
+    float* o_part;
+    float* lse_part;
+    int splits, tps;
+};
+
+template <int BN, bool CAUSAL>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fwd_kernel_split(Fav4Args a, SplitArgs sp, int tiles, int total) {
+    constexpr int WAVES = 8, BM = 256;
+    constexpr int TILE_BYTES = BN * ROW_BYTES;
+    constexpr int STAGE_BYTES = 2 * TILE_BYTES;
+    constexpr int DMA = BN / 4 / WAVES;
+    static_assert(BN % 32 == 0 && BN % (4 * WAVES) == 0, "tile shape");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 31, half = lane >> 5;
+    const uint32_t row_bytes = uint32_t(a.heads) * ROW_BYTES;
+    const float scale2 = a.scale * LOG2E;
+    const uint32_t smem_base = lds_addr(smem);
+    const int bhs = a.batch * a.heads;
+
+    LdsOffsets off;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) off.k[c] = col * ROW_BYTES + ((((2 * c) | half) ^ k_swz(col)) << 4);
+    {
+        const int r0 = half * 4 + ((lane & 15) >> 2);
+        const int gl = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r = r0 + 8 * j;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+                off.v[j][db] = r * ROW_BYTES + (((db * 4 + gl) ^ v_swz(r)) << 4) + ((lane & 1) << 3);
+        }
+    }
+    uint32_t dk[DMA], dv[DMA];
+#pragma unroll
+    for (int i = 0; i < DMA; ++i) {
+        const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
+        dk[i] = r * row_bytes + ((p ^ k_swz(r)) << 4);
+        dv[i] = r * row_bytes + ((p ^ v_swz(r)) << 4);
+    }
+
+    for (int id = blockIdx.x; id < total; id += gridDim.x) {
+        // XCD-contiguous order; within a (b, h) the q tiles of one key chunk
+        // are adjacent, so they share that chunk in L2.
+        const int xcd = id & 7, slot = id >> 3, per = total >> 3, rem = total & 7;
+        const int logical = xcd * per + min(xcd, rem) + slot;
+        const int per_bh = tiles * sp.splits;
+        const int bh = __builtin_amdgcn_readfirstlane(logical / per_bh);
+        const int r = __builtin_amdgcn_readfirstlane(logical - bh * per_bh);
+        const int split = r / tiles, tile = r - split * tiles;
+
+        const int batch = bh / a.heads, head = bh - batch * a.heads;
+        const int q0 = tile * BM, qw = q0 + wave * 32;
+        const int row = qw + col;
+        const int64_t qrow0 = (int64_t(batch) * a.sq + q0) * a.heads + head;
+        const int64_t krow0 = int64_t(batch) * a.sk * a.heads + head;
+        const char* kbase = static_cast<const char*>(a.k) + krow0 * ROW_BYTES;
+        const char* vbase = static_cast<const char*>(a.v) + krow0 * ROW_BYTES;
+        const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + qrow0 * ROW_BYTES,
+                                    uint32_t(a.sq - q0 - 1) * row_bytes + ROW_BYTES);
+        // This chunk's rows of o_part: [sq - q0 rows][128] FP32 from row q0.
+        const int64_t prow0 = (int64_t(split) * bhs + bh) * a.sq + q0;
+        const rsrc_t rp = make_rsrc(sp.o_part + prow0 * D, uint32_t(a.sq - q0) * D * 4);
+        const int kend = CAUSAL ? min(a.sk, q0 + BM) : a.sk;
+        const int ntiles = (kend + BN - 1) / BN;
+        const int nfull = (CAUSAL ? min(a.sk, q0 + 1) : a.sk) / BN;
+        const int t0 = split * sp.tps, t1 = min(ntiles, t0 + sp.tps);
+
+        RowState st;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) st.o[db] = f32x16{};
+        st.m = -__builtin_inff();
+        st.lb = 0.f;
+        st.l = 0.f;
+
+        if (t0 < t1) {
+            // DMA of key tile t into stage (t - t0) & 1.
+            auto issue = [&](int t) {
+                const int64_t first = int64_t(t) * BN;
+                const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * row_bytes + ROW_BYTES;
+                const u32x4 rk = make_desc(kbase + first * row_bytes, bytes);
+                const u32x4 rv = make_desc(vbase + first * row_bytes, bytes);
+                const uint32_t ks = smem_base + ((t - t0) & 1) * STAGE_BYTES + wave * DMA * 1024;
+#pragma unroll
+                for (int i = 0; i < DMA; ++i) {
+                    dma16(rk, ks + i * 1024, dk[i]);
+                    dma16(rv, ks + TILE_BYTES + i * 1024, dv[i]);
+                }
+            };
+            issue(t0);
+            bf16x8 qr[8];
+            {
+                const uint32_t qoff = uint32_t(wave * 32 + col) * row_bytes + half * 16;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) qr[c] = load16(rq, qoff + c * 32);
+#pragma unroll
+                for (int c = 0; c < 8; ++c) asm volatile("" ::"v"(qr[c]));
+            }
+            auto step = [&](auto stage_c, auto masked_c, int t) {
+                constexpr int STAGE = decltype(stage_c)::value;
+                const unsigned char* cur = smem + STAGE * STAGE_BYTES;
+                wait_vmem();
+                __syncthreads();
+                if (t + 1 < t1) issue(t + 1);
+                attend_fused<BN, decltype(masked_c)::value, CAUSAL, true, CAUSAL>(
+                    cur, cur + TILE_BYTES, off, qr, st, t == t0, t * BN, a.sk, qw, row, half, scale2);
+            };
+            using S0 = std::integral_constant<int, 0>;
+            using S1 = std::integral_constant<int, 1>;
+            using Plain = std::integral_constant<bool, false>;
+            using Masked = std::integral_constant<bool, true>;
+            int t = t0;
+            const int tp = min(t1, nfull);
+            for (; t + 1 < tp; t += 2) {
+                step(S0{}, Plain{}, t);
+                step(S1{}, Plain{}, t + 1);
+            }
+            for (; t < t1; ++t) {
+                if ((t - t0) & 1) step(S1{}, Masked{}, t);
+                else step(S0{}, Masked{}, t);
+            }
+        }
+
+        // Chunk epilogue: FP32 O / lb and the two log2-domain sums.
+        const float inv = st.lb > 0.f ? 1.f / st.lb : 0.f;
+        const uint32_t pbase = uint32_t(wave * 32 + col) * (D * 4) + half * 16;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+#pragma unroll
+            for (int vg = 0; vg < 4; ++vg) {
+                const f32x4 x = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv,
+                                 st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
+                store16(rp, pbase + (db * 32 + vg * 8) * 4, x);
+            }
+        }
+        if (half == 0 && row < a.sq) {
+            float* lp = sp.lse_part + ((int64_t(split) * bhs + bh) * a.sq + row) * 2;
+            lp[0] = st.m + __builtin_amdgcn_logf(st.lb);
+            lp[1] = st.m + __builtin_amdgcn_logf(st.l);
+        }
+        wait_vmem();
+        __syncthreads();
+    }
+}
+
+// Merge of the split-KV chunks: one 32-lane group per (b, h, row), 4 output
+// dims per lane; O in BF16 BSHD and the optional FP32 LSE.
+__global__ __launch_bounds__(256) void combine_kernel(Fav4Args a, SplitArgs sp) {
+    const int64_t rows = int64_t(a.batch) * a.heads * a.sq;
+    const int64_t r = int64_t(blockIdx.x) * 8 + (threadIdx.x >> 5);
+    const int q4 = threadIdx.x & 31;
+    if (r >= rows) return;
+    const int64_t bh = r / a.sq;
+    const int row = int(r - bh * a.sq);
+    const int64_t slab = rows;                      // rows per chunk
+    float mb = -__builtin_inff(), ml = -__builtin_inff();
+    for (int s = 0; s < sp.splits; ++s) {
+        const float* lp = sp.lse_part + (s * slab + r) * 2;
+        mb = fmaxf(mb, lp[0]);
+        ml = fmaxf(ml, lp[1]);
+    }
+    float den = 0.f, suml = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < sp.splits; ++s) {
+        const float* lp = sp.lse_part + (s * slab + r) * 2;
+        const float w = exp2_native(lp[0] - mb);
+        suml += exp2_native(lp[1] - ml);
+        if (w > 0.f) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(sp.o_part + (s * slab + r) * D + q4 * 4);
+            acc += w * x;
+            den += w;
+        }
+    }
+    const f32x4 y = acc * (1.f / den);
+    const int batch = int(bh / a.heads), head = int(bh - int64_t(batch) * a.heads);
+    const int64_t orow = (int64_t(batch) * a.sq + row) * a.heads + head;
+    const f32x2 y0 = {y[0], y[1]}, y1 = {y[2], y[3]};
+    const bf16x2 b0 = __builtin_convertvector(y0, bf16x2), b1 = __builtin_convertvector(y1, bf16x2);
+    *reinterpret_cast<bf16x4*>(static_cast<char*>(a.o) + orow * ROW_BYTES + q4 * 8) = bf16x4{b0[0], b0[1], b1[0], b1[1]};
+    if (a.lse && q4 == 0) a.lse[r] = (ml + __builtin_amdgcn_logf(suml)) * LN2;
 }
 
 }  // namespace fav4

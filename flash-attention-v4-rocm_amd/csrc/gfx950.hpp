@@ -95,6 +95,10 @@ __device__ __forceinline__ void store8(rsrc_t r, uint32_t voffset, bf16x4 v) {
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, voffset, 0, 0);
 }
 
+__device__ __forceinline__ void store16(rsrc_t r, uint32_t voffset, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voffset, 0, 0);
+}
+
 __device__ __forceinline__ bf16x8 lds_read16(const void* lds) {
     return *reinterpret_cast<const FAV4_LDS bf16x8*>((FAV4_LDS const void*)lds);
 }

@@ -66,6 +66,13 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
         lib.fav4_bshd_forward.restype = C.c_int
         lib.fav4_bshd_select_config.argtypes = [C.POINTER(Args)]
         lib.fav4_bshd_select_config.restype = C.c_int
+        lib.fav4_bshd_forward_splitkv.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_void_p, C.c_size_t,
+                                                  C.c_void_p]
+        lib.fav4_bshd_forward_splitkv.restype = C.c_int
+        lib.fav4_bshd_splitkv_workspace_size.argtypes = [C.POINTER(Args), C.c_int, C.c_int]
+        lib.fav4_bshd_splitkv_workspace_size.restype = C.c_longlong
+        lib.fav4_bshd_splitkv_select.argtypes = [C.POINTER(Args), C.c_int]
+        lib.fav4_bshd_splitkv_select.restype = C.c_int
         _LIB = lib
     return _LIB
 
@@ -101,6 +108,37 @@ class Runner:
         b, sq, h, _ = q.shape
         a = Args(None, None, None, None, None, b, h, sq, k.shape[1], 1 / math.sqrt(D))
         return self.hip.fav4_bshd_select_config(C.byref(a))
+
+    # ---- split-KV (fav4_bshd_forward_splitkv; no reference counterpart) ----
+    @staticmethod
+    def shape_args(batch, heads, sq, sk) -> Args:
+        return Args(None, None, None, None, None, batch, heads, sq, sk, 1 / math.sqrt(D))
+
+    def splitkv_select(self, batch, heads, sq, sk, causal) -> int:
+        return self.hip.fav4_bshd_splitkv_select(C.byref(self.shape_args(batch, heads, sq, sk)), int(causal))
+
+    def splitkv_workspace_size(self, batch, heads, sq, sk, causal, splits=0) -> int:
+        a = self.shape_args(batch, heads, sq, sk)
+        return self.hip.fav4_bshd_splitkv_workspace_size(C.byref(a), int(causal), int(splits))
+
+    def call_splitkv(self, q, k, v, o, lse, causal, splits=0, workspace=None, scale=None, stream=None):
+        """Split-KV forward.  `workspace` is a CUDA tensor (any dtype, 256-byte aligned);
+        None allocates one of the required size here (the library never allocates)."""
+        import torch
+        a = self.args(q, k, v, o, lse, scale)
+        if workspace is None:
+            need = self.hip.fav4_bshd_splitkv_workspace_size(C.byref(a), int(causal), int(splits))
+            if need < 0:
+                raise RuntimeError(f"splits {splits}: arguments rejected")
+            workspace = torch.empty(max(need, 1), device=q.device, dtype=torch.uint8)
+        nbytes = workspace.numel() * workspace.element_size()
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
+        status = self.hip.fav4_bshd_forward_splitkv(C.byref(a), int(causal), int(splits), workspace.data_ptr(),
+                                                     nbytes, stream)
+        if status:
+            raise RuntimeError(f"splitkv splits {splits}: HIP status {status}")
+        return workspace
 
 
 def forward(q, k, v, causal=False, with_lse=False, config=0, scale=None):

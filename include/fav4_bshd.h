@@ -40,3 +40,27 @@ extern "C" int fav4_bshd_forward(const Fav4Args* args, int causal, int config, h
 // Replaces include/fav4_bshd.h:20 (fav4_bshd_select_config): the config ID
 // that config 0 resolves to for these arguments (-1 for a NULL pointer).
 extern "C" int fav4_bshd_select_config(const Fav4Args* args);
+
+// ---- Split-KV forward --------------------------------------------------------
+// No counterpart in the reference.  It is for callers whose B * H * ceil(Sq/256)
+// work items are too few to fill the GPU while Sk is long: each item's key
+// range is cut into `splits` chunks attended in parallel, then merged by their
+// log-sum-exp.  Results match fav4_bshd_forward within the same tolerances
+// (not bitwise: the chunks' BF16 weights are rounded against their own base).
+// Same argument contract as fav4_bshd_forward (config is always Auto), plus:
+//  * splits: 0 = library choice (about two workgroups per CU, >= 256 keys per
+//    chunk, at most 64 chunks), else 1..256 (clamped to the key tiles);
+//    splits resolving to 1 run fav4_bshd_forward and need no workspace;
+//  * workspace: caller-owned device memory, 256-byte aligned, at least
+//    fav4_bshd_splitkv_workspace_size() bytes, not shared with a concurrent
+//    call; its contents on entry do not matter and are scratch afterwards;
+//  * Sq <= 2^22.
+// Returns 0, hipErrorInvalidValue (1) for rejected arguments or a missing /
+// small / misaligned workspace, else the launch status.  Allocates nothing.
+extern "C" int fav4_bshd_forward_splitkv(const Fav4Args* args, int causal, int splits, void* workspace,
+                                         size_t workspace_bytes, hipStream_t stream);
+// Workspace bytes fav4_bshd_forward_splitkv needs for these arguments and
+// `splits` (0 when it needs none), or -1 for rejected arguments.
+extern "C" long long fav4_bshd_splitkv_workspace_size(const Fav4Args* args, int causal, int splits);
+// The chunk count that splits = 0 resolves to (1 = no split), or -1.
+extern "C" int fav4_bshd_splitkv_select(const Fav4Args* args, int causal);

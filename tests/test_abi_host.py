@@ -1,9 +1,11 @@
 """Host-only checks of the C ABI (no GPU needed, no compute call is made).
 
-The library must export exactly the two entry points of the reference header
-(include/fav4_bshd.h:19-20), lay out Fav4Args byte for byte like it
-(include/fav4_bshd.h:4-10), and reject bad arguments with
-hipErrorInvalidValue before touching HIP, as src/bshd.hip:27-34 does.
+The library must export the two entry points of the reference header
+(include/fav4_bshd.h:19-20) plus the three split-KV ones of this build, lay
+out Fav4Args byte for byte like the reference (include/fav4_bshd.h:4-10), and
+reject bad arguments with hipErrorInvalidValue before touching HIP, as
+src/bshd.hip:27-34 does.  The split-KV size / plan queries are checked
+against their closed forms.
 """
 import ctypes as C
 import math
@@ -43,7 +45,8 @@ def test_exports_exactly_the_c_abi():
                          check=True).stdout
     names = {line.split()[-1] for line in out.splitlines() if line.strip()}
     public = {n for n in names if not n.startswith("_")}
-    assert public == {"fav4_bshd_forward", "fav4_bshd_select_config"}, public
+    assert public == {"fav4_bshd_forward", "fav4_bshd_select_config", "fav4_bshd_forward_splitkv",
+                      "fav4_bshd_splitkv_workspace_size", "fav4_bshd_splitkv_select"}, public
 
 
 def test_ctypes_layout_matches_reference(Args):
@@ -94,6 +97,8 @@ def test_rejects_bad_arguments(lib, Args, name, change):
     fields.update(change)
     a = Args(**fields)
     assert lib.fav4_bshd_forward(C.byref(a), 0, 0, None) == HIP_ERROR_INVALID_VALUE
+    # the split-KV entry point applies the same checks first (a valid workspace pointer given)
+    assert lib.fav4_bshd_forward_splitkv(C.byref(a), 0, 4, 0x100000, 1 << 30, None) == HIP_ERROR_INVALID_VALUE
 
 
 @pytest.mark.parametrize("causal,config", [(-1, 0), (2, 0), (0, -1), (0, 4), (1, 7)])
@@ -124,3 +129,73 @@ def test_runner_rejects_host_tensors():
         runner.args(q, q, q, q, None)
     with pytest.raises(AssertionError):
         runner.args(q.float(), q, q, q, None)
+
+
+# ---- split-KV queries -------------------------------------------------------
+
+def _split_plan(b, h, sq, sk, splits, cus=None, causal=False):
+    """Closed form of the split plan: 64-key tiles over the keys a row can see
+    (min(sk, sq) for top-left causal), 256-row q tiles; splits=0 picks
+    ceil(2*CUs / items) capped by min(64, ktiles // 4); then tiles-per-chunk and the
+    final count so that no chunk is empty."""
+    ktiles = -(-(min(sk, sq) if causal else sk) // 64)
+    if splits == 0:
+        items = b * h * -(-sq // 256)
+        splits = min(-(-2 * cus // items), min(64, max(1, ktiles // 4)))
+    splits = max(1, min(splits, ktiles))
+    tps = -(-ktiles // splits)
+    return -(-ktiles // tps), tps
+
+
+@pytest.mark.parametrize("shape,splits", [((2, 3, 300, 5000), 5), ((1, 8, 1024, 32768), 16), ((1, 1, 1, 64), 8),
+                                          ((4, 2, 257, 1000), 3), ((1, 2, 100, 129), 256), ((3, 1, 70, 4097), 7)])
+def test_splitkv_workspace_size_closed_form(lib, Args, shape, splits):
+    b, h, sq, sk = shape
+    a = Args(None, None, None, None, None, b, h, sq, sk, 1 / math.sqrt(128))
+    for causal in (0, 1):
+        n, _ = _split_plan(b, h, sq, sk, splits, causal=bool(causal))
+        want = 0 if n == 1 else n * b * h * sq * (128 * 4 + 8)
+        assert lib.fav4_bshd_splitkv_workspace_size(C.byref(a), causal, splits) == want
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 1024, 32768), (32, 8, 4096, 4096), (1, 1, 256, 65536), (2, 4, 512, 2048),
+                                   (1, 1, 100, 100)])
+def test_splitkv_auto_plan(lib, Args, shape):
+    """Auto chunk count, for the CU count the library sees (256 on MI355X; the
+    same fallback when no device is visible)."""
+    b, h, sq, sk = shape
+    a = Args(None, None, None, None, None, b, h, sq, sk, 1 / math.sqrt(128))
+    for causal in (0, 1):
+        n, _ = _split_plan(b, h, sq, sk, 0, cus=256, causal=bool(causal))
+        assert lib.fav4_bshd_splitkv_select(C.byref(a), causal) == n
+        want = 0 if n == 1 else n * b * h * sq * (128 * 4 + 8)
+        assert lib.fav4_bshd_splitkv_workspace_size(C.byref(a), causal, 0) == want
+
+
+def test_splitkv_plan_examples():
+    # B1 H8 Sq1024 Sk32768 (32 items, 512 key tiles): 16 chunks of 32 tiles;
+    # the headline B32 H8 S4096 needs no split; 79 key tiles in 5 chunks of 16.
+    assert _split_plan(1, 8, 1024, 32768, 0, cus=256) == (16, 32)
+    assert _split_plan(32, 8, 4096, 4096, 0, cus=256)[0] == 1
+    assert _split_plan(2, 3, 300, 5000, 5) == (5, 16)
+    assert _split_plan(1, 1, 256, 65536, 0, cus=256) == (64, 16)
+    # causal B1 H8 Sq1024 Sk32768 sees only the first 1024 keys: 4 chunks of 4 tiles
+    assert _split_plan(1, 8, 1024, 32768, 0, cus=256, causal=True) == (4, 4)
+
+
+@pytest.mark.parametrize("causal,splits,sq", [(2, 4, 256), (-1, 4, 256), (0, -1, 256), (0, 257, 256),
+                                              (0, 4, (1 << 22) + 1)])
+def test_splitkv_queries_reject(lib, Args, causal, splits, sq):
+    a = Args(None, None, None, None, None, 1, 1, sq, 4096, 1 / math.sqrt(128))
+    assert lib.fav4_bshd_splitkv_workspace_size(C.byref(a), causal, splits) == -1
+    assert lib.fav4_bshd_splitkv_workspace_size(None, 0, 0) == -1
+    assert lib.fav4_bshd_splitkv_select(None, 0) == -1
+
+
+@pytest.mark.parametrize("ws,nbytes", [(None, 1 << 30), (0x100010, 1 << 30), (0x100000, 1000)],
+                         ids=["null", "misaligned", "too_small"])
+def test_splitkv_rejects_workspace(lib, Args, ws, nbytes):
+    fields = _good(Args)
+    fields.update(sq=256, sk=8192)
+    a = Args(**fields)
+    assert lib.fav4_bshd_forward_splitkv(C.byref(a), 0, 8, ws, nbytes, None) == HIP_ERROR_INVALID_VALUE
