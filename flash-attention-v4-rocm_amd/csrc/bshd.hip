@@ -17,7 +17,7 @@ namespace {
 constexpr int64_t MAX_GRID = int64_t(1) << 22;
 
 template <int WAVES, int BN, int STAGES, bool PIPE, bool CAUSAL>
-int launch(const Fav4Args& a, hipStream_t stream) {
+int launch(const Fav4Args& a, int kv_heads, hipStream_t stream) {
     constexpr int BM = WAVES * 32;
     const int tiles = (a.sq + BM - 1) / BM;
     const int64_t total = int64_t(fav4::items_per_head<CAUSAL>(tiles)) * a.batch * a.heads;
@@ -25,19 +25,19 @@ int launch(const Fav4Args& a, hipStream_t stream) {
     const int grid = int(total < MAX_GRID ? total : MAX_GRID);
     if (a.lse)
         hipLaunchKernelGGL((fav4::fwd_kernel<WAVES, BN, CAUSAL, true, STAGES, PIPE>), dim3(grid),
-                           dim3(WAVES * 64), 0, stream, a, tiles, int(total));
+                           dim3(WAVES * 64), 0, stream, a, kv_heads, tiles, int(total));
     else
         hipLaunchKernelGGL((fav4::fwd_kernel<WAVES, BN, CAUSAL, false, STAGES, PIPE>), dim3(grid),
-                           dim3(WAVES * 64), 0, stream, a, tiles, int(total));
+                           dim3(WAVES * 64), 0, stream, a, kv_heads, tiles, int(total));
     return hipGetLastError();
 }
 
 template <bool CAUSAL>
-int dispatch(const Fav4Args& a, int config, hipStream_t stream) {
+int dispatch(const Fav4Args& a, int kv_heads, int config, hipStream_t stream) {
     switch (config) {
-    case 1: return launch<4, 64, 2, false, CAUSAL>(a, stream);
-    case 2: return launch<8, 64, 2, false, CAUSAL>(a, stream);
-    case 3: return launch<8, 64, 3, true, CAUSAL>(a, stream);
+    case 1: return launch<4, 64, 2, false, CAUSAL>(a, kv_heads, stream);
+    case 2: return launch<8, 64, 2, false, CAUSAL>(a, kv_heads, stream);
+    case 3: return launch<8, 64, 3, true, CAUSAL>(a, kv_heads, stream);
     default: return hipErrorInvalidValue;
     }
 }
@@ -124,8 +124,8 @@ int launch_split(const Fav4Args& a, const SplitPlan& p, void* ws, hipStream_t st
     sp.splits = p.splits;
     sp.tps = p.tps;
     const int grid = int(total < MAX_GRID ? total : MAX_GRID);
-    hipLaunchKernelGGL((fav4::fwd_kernel_split<SPLIT_BN, CAUSAL>), dim3(grid), dim3(512), 0, stream, a, sp, tiles,
-                       int(total));
+    hipLaunchKernelGGL((fav4::fwd_kernel_split<SPLIT_BN, CAUSAL>), dim3(grid), dim3(512), 0, stream, a, sp, a.heads,
+                       tiles, int(total));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(fav4::combine_kernel, dim3(unsigned((rows + 7) / 8)), dim3(256), 0, stream, a, sp);
@@ -147,7 +147,17 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward(const Fa
     const int st = validate(a, causal, config);
     if (st != hipSuccess) return st;
     if (config == 0) config = fav4_bshd_select_config(a);
-    return causal ? dispatch<true>(*a, config, stream) : dispatch<false>(*a, config, stream);
+    return causal ? dispatch<true>(*a, a->heads, config, stream) : dispatch<false>(*a, a->heads, config, stream);
+}
+
+// Grouped-query / multi-query attention (no counterpart in the reference).
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_gqa(const Fav4Args* a, int kv_heads,
+                                                                    int causal, int config, hipStream_t stream) {
+    const int st = validate(a, causal, config);
+    if (st != hipSuccess) return st;
+    if (kv_heads <= 0 || kv_heads > a->heads || a->heads % kv_heads != 0) return hipErrorInvalidValue;
+    if (config == 0) config = fav4_bshd_select_config(a);
+    return causal ? dispatch<true>(*a, kv_heads, config, stream) : dispatch<false>(*a, kv_heads, config, stream);
 }
 
 // Split-KV entry points (no counterpart in the reference; see the header).

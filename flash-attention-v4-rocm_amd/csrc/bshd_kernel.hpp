@@ -309,7 +309,7 @@ __device__ __forceinline__ void pv_plain(const unsigned char* vs, const LdsOffse
 // stage.  Masked tiles (causal diagonal, key tail) follow unpipelined.
 template <int WAVES, int BN, bool CAUSAL, bool LSE, int STAGES, bool PIPE = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void fwd_kernel(Fav4Args a, int tiles, int total) {
+void fwd_kernel(Fav4Args a, int kv_heads, int tiles, int total) {
     static_assert(!PIPE || STAGES == 3, "the cross-tile pipeline keeps three tiles in LDS");
     constexpr int BM = WAVES * 32;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
@@ -323,7 +323,9 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 31, half = lane >> 5;
-    const uint32_t row_bytes = uint32_t(a.heads) * ROW_BYTES;   // stride between sequence positions
+    const uint32_t row_bytes = uint32_t(a.heads) * ROW_BYTES;   // Q/O stride between sequence positions
+    const uint32_t kv_row_bytes = uint32_t(kv_heads) * ROW_BYTES;   // K/V stride (kv_heads divides heads)
+    const int group = a.heads / kv_heads;                           // query heads per K/V head
     const float scale2 = a.scale * LOG2E;
     const uint32_t smem_base = lds_addr(smem);
 
@@ -346,8 +348,8 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
 #pragma unroll
     for (int i = 0; i < DMA; ++i) {
         const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
-        dk[i] = r * row_bytes + ((p ^ k_swz(r)) << 4);
-        dv[i] = r * row_bytes + ((p ^ v_swz(r)) << 4);
+        dk[i] = r * kv_row_bytes + ((p ^ k_swz(r)) << 4);
+        dv[i] = r * kv_row_bytes + ((p ^ v_swz(r)) << 4);
     }
 
     auto process = [&](int bh, int tile) {
@@ -355,7 +357,7 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
         const int q0 = tile * BM, qw = q0 + wave * 32;
         const int row = qw + col;                                 // this lane's query row
         const int64_t qrow0 = (int64_t(batch) * a.sq + q0) * a.heads + head;
-        const int64_t krow0 = int64_t(batch) * a.sk * a.heads + head;
+        const int64_t krow0 = int64_t(batch) * a.sk * kv_heads + head / group;
         const char* kbase = static_cast<const char*>(a.k) + krow0 * ROW_BYTES;
         const char* vbase = static_cast<const char*>(a.v) + krow0 * ROW_BYTES;
         const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + qrow0 * ROW_BYTES,
@@ -375,9 +377,9 @@ void fwd_kernel(Fav4Args a, int tiles, int total) {
         auto issue = [&](int t) {
             const int tc = min(t, ntiles - 1);
             const int64_t first = int64_t(tc) * BNT;
-            const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * row_bytes + ROW_BYTES;
-            const u32x4 rk = make_desc(kbase + first * row_bytes, bytes);
-            const u32x4 rv = make_desc(vbase + first * row_bytes, bytes);
+            const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * kv_row_bytes + ROW_BYTES;
+            const u32x4 rk = make_desc(kbase + first * kv_row_bytes, bytes);
+            const u32x4 rv = make_desc(vbase + first * kv_row_bytes, bytes);
             const uint32_t ks = smem_base + (t % STAGES) * STAGE_BYTES + wave * DMA * 1024;
 #pragma unroll
             for (int i = 0; i < DMA; ++i) {
@@ -569,7 +571,7 @@ struct SplitArgs {
 
 template <int BN, bool CAUSAL>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void fwd_kernel_split(Fav4Args a, SplitArgs sp, int tiles, int total) {
+void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int total) {
     constexpr int WAVES = 8, BM = 256;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
     constexpr int STAGE_BYTES = 2 * TILE_BYTES;
@@ -581,6 +583,8 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int tiles, int total) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 31, half = lane >> 5;
     const uint32_t row_bytes = uint32_t(a.heads) * ROW_BYTES;
+    const uint32_t kv_row_bytes = uint32_t(kv_heads) * ROW_BYTES;
+    const int group = a.heads / kv_heads;
     const float scale2 = a.scale * LOG2E;
     const uint32_t smem_base = lds_addr(smem);
     const int bhs = a.batch * a.heads;
@@ -603,8 +607,8 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int tiles, int total) {
 #pragma unroll
     for (int i = 0; i < DMA; ++i) {
         const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
-        dk[i] = r * row_bytes + ((p ^ k_swz(r)) << 4);
-        dv[i] = r * row_bytes + ((p ^ v_swz(r)) << 4);
+        dk[i] = r * kv_row_bytes + ((p ^ k_swz(r)) << 4);
+        dv[i] = r * kv_row_bytes + ((p ^ v_swz(r)) << 4);
     }
 
     for (int id = blockIdx.x; id < total; id += gridDim.x) {
@@ -621,7 +625,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int tiles, int total) {
         const int q0 = tile * BM, qw = q0 + wave * 32;
         const int row = qw + col;
         const int64_t qrow0 = (int64_t(batch) * a.sq + q0) * a.heads + head;
-        const int64_t krow0 = int64_t(batch) * a.sk * a.heads + head;
+        const int64_t krow0 = int64_t(batch) * a.sk * kv_heads + head / group;
         const char* kbase = static_cast<const char*>(a.k) + krow0 * ROW_BYTES;
         const char* vbase = static_cast<const char*>(a.v) + krow0 * ROW_BYTES;
         const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + qrow0 * ROW_BYTES,
@@ -645,9 +649,9 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int tiles, int total) {
             // DMA of key tile t into stage (t - t0) & 1.
             auto issue = [&](int t) {
                 const int64_t first = int64_t(t) * BN;
-                const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * row_bytes + ROW_BYTES;
-                const u32x4 rk = make_desc(kbase + first * row_bytes, bytes);
-                const u32x4 rv = make_desc(vbase + first * row_bytes, bytes);
+                const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * kv_row_bytes + ROW_BYTES;
+                const u32x4 rk = make_desc(kbase + first * kv_row_bytes, bytes);
+                const u32x4 rv = make_desc(vbase + first * kv_row_bytes, bytes);
                 const uint32_t ks = smem_base + ((t - t0) & 1) * STAGE_BYTES + wave * DMA * 1024;
 #pragma unroll
                 for (int i = 0; i < DMA; ++i) {

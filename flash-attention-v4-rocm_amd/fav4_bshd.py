@@ -73,6 +73,8 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
         lib.fav4_bshd_splitkv_workspace_size.restype = C.c_longlong
         lib.fav4_bshd_splitkv_select.argtypes = [C.POINTER(Args), C.c_int]
         lib.fav4_bshd_splitkv_select.restype = C.c_int
+        lib.fav4_bshd_forward_gqa.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_int, C.c_void_p]
+        lib.fav4_bshd_forward_gqa.restype = C.c_int
         _LIB = lib
     return _LIB
 
@@ -83,11 +85,12 @@ class Runner:
     def __init__(self, path: Path = LIB_PATH):
         self.hip = load_library(path)
 
-    def args(self, q, k, v, o, lse, scale=None) -> Args:
+    def args(self, q, k, v, o, lse, scale=None, kv_heads=None) -> Args:
         import torch
         assert all(x.dtype == torch.bfloat16 and x.is_cuda and x.is_contiguous() for x in (q, k, v, o))
         b, sq, h, d = q.shape
-        assert d == D and k.shape == v.shape and k.shape[0] == b and tuple(k.shape[2:]) == (h, d)
+        kvh = h if kv_heads is None else kv_heads
+        assert d == D and k.shape == v.shape and k.shape[0] == b and tuple(k.shape[2:]) == (kvh, d)
         assert o.shape == q.shape
         assert lse is None or (tuple(lse.shape) == (b, h, sq) and lse.is_contiguous()
                                and lse.dtype == torch.float32)
@@ -103,6 +106,16 @@ class Runner:
         status = self.hip.fav4_bshd_forward(C.byref(a), int(causal), int(config), stream)
         if status:
             raise RuntimeError(f"config {config}: HIP status {status}")
+
+    def call_gqa(self, q, k, v, o, lse, causal, config=0, scale=None, stream=None):
+        """fav4_bshd_forward_gqa: K/V heads = k.shape[2] (must divide q's heads)."""
+        import torch
+        a = self.args(q, k, v, o, lse, scale, kv_heads=k.shape[2])
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
+        status = self.hip.fav4_bshd_forward_gqa(C.byref(a), int(k.shape[2]), int(causal), int(config), stream)
+        if status:
+            raise RuntimeError(f"gqa config {config}: HIP status {status}")
 
     def select_config(self, q, k) -> int:
         b, sq, h, _ = q.shape

@@ -64,3 +64,13 @@ extern "C" int fav4_bshd_forward_splitkv(const Fav4Args* args, int causal, int s
 extern "C" long long fav4_bshd_splitkv_workspace_size(const Fav4Args* args, int causal, int splits);
 // The chunk count that splits = 0 resolves to (1 = no split), or -1.
 extern "C" int fav4_bshd_splitkv_select(const Fav4Args* args, int causal);
+
+// ---- Grouped-query / multi-query attention ----------------------------------
+// No counterpart in the reference (its README lists GQA as unsupported).  The
+// same contract as fav4_bshd_forward, except that K and V are
+// [batch, sk, kv_heads, 128] with kv_heads dividing heads: query head h reads
+// K/V head h / (heads / kv_heads).  kv_heads == heads is exactly
+// fav4_bshd_forward.  Returns hipErrorInvalidValue also for kv_heads <= 0,
+// kv_heads > heads or heads % kv_heads != 0.
+extern "C" int fav4_bshd_forward_gqa(const Fav4Args* args, int kv_heads, int causal, int config,
+                                     hipStream_t stream);

@@ -46,7 +46,7 @@ def test_exports_exactly_the_c_abi():
     names = {line.split()[-1] for line in out.splitlines() if line.strip()}
     public = {n for n in names if not n.startswith("_")}
     assert public == {"fav4_bshd_forward", "fav4_bshd_select_config", "fav4_bshd_forward_splitkv",
-                      "fav4_bshd_splitkv_workspace_size", "fav4_bshd_splitkv_select"}, public
+                      "fav4_bshd_splitkv_workspace_size", "fav4_bshd_splitkv_select", "fav4_bshd_forward_gqa"}, public
 
 
 def test_ctypes_layout_matches_reference(Args):
@@ -97,8 +97,9 @@ def test_rejects_bad_arguments(lib, Args, name, change):
     fields.update(change)
     a = Args(**fields)
     assert lib.fav4_bshd_forward(C.byref(a), 0, 0, None) == HIP_ERROR_INVALID_VALUE
-    # the split-KV entry point applies the same checks first (a valid workspace pointer given)
+    # the split-KV and GQA entry points apply the same checks first
     assert lib.fav4_bshd_forward_splitkv(C.byref(a), 0, 4, 0x100000, 1 << 30, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_forward_gqa(C.byref(a), 1, 0, 0, None) == HIP_ERROR_INVALID_VALUE
 
 
 @pytest.mark.parametrize("causal,config", [(-1, 0), (2, 0), (0, -1), (0, 4), (1, 7)])
@@ -199,3 +200,12 @@ def test_splitkv_rejects_workspace(lib, Args, ws, nbytes):
     fields.update(sq=256, sk=8192)
     a = Args(**fields)
     assert lib.fav4_bshd_forward_splitkv(C.byref(a), 0, 8, ws, nbytes, None) == HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.parametrize("kv_heads", [0, -1, 5, 3, 8])
+def test_gqa_rejects_bad_kv_heads(lib, Args, kv_heads):
+    """heads = 4: kv_heads must be a positive divisor of it."""
+    a = Args(**_good(Args))
+    assert lib.fav4_bshd_forward_gqa(C.byref(a), kv_heads, 0, 0, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_forward_gqa(C.byref(a), 2, 2, 0, None) == HIP_ERROR_INVALID_VALUE   # bad causal
+    assert lib.fav4_bshd_forward_gqa(None, 2, 0, 0, None) == HIP_ERROR_INVALID_VALUE
