@@ -62,6 +62,8 @@ def parse_args():
     p.add_argument("--sweep", default="", help="comma list of extra sequence lengths to time (report only)")
     p.add_argument("--no-comparator", action="store_true", help="skip the torch SDPA comparator")
     p.add_argument("--no-splitkv", action="store_true", help="skip the split-KV report (B1 H8 Sq1024 Sk32768)")
+    p.add_argument("--no-telemetry", action="store_true",
+                   help="start no child processes (amd-smi clocks, hipcc version), e.g. under a profiler")
     p.add_argument("--pmc-pass", action="store_true",
                    help="profiling mode for counter runs: two eager launches per mask type, then a "
                         "plain 1 GiB device copy (HBM counter calibration); prints no JSON")
@@ -269,8 +271,13 @@ def splitkv_report(torch, orc, runner, args, stream, b=1, h=8, sq=1024, sk=32768
     return out
 
 
+_TELEMETRY = True
+
+
 def _run(cmd, timeout=20):
     import subprocess
+    if not _TELEMETRY:
+        return None
     try:
         r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
         return r.stdout if r.returncode == 0 else None
@@ -347,6 +354,8 @@ def read_traffic():
 
 def main():
     args = parse_args()
+    global _TELEMETRY
+    _TELEMETRY = not args.no_telemetry
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}))
@@ -408,7 +417,7 @@ def main():
 
     dense = results[False]
     clk = loaded_gfx_clock(torch, lambda: runner.call(q, k, v, o, None, False, args.config,
-                                                      stream=stream.cuda_stream), stream)
+                                                      stream=stream.cuda_stream), stream) if _TELEMETRY else None
     traffic = read_traffic()
     compulsory = 2 * b * h * 128 * (2 * s + 2 * s)
     roofline = dict(bound="mfma", achieved=round(dense["tflops"], 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
