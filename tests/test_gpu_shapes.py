@@ -140,3 +140,16 @@ def test_bad_arguments_return_status(gpu_runner):
         gpu_runner.call(q, k, v, o, None, 0, 0, scale=float("nan"))
     torch.cuda.synchronize()
     assert torch.isnan(o).all().item()
+
+
+def test_tensors_past_4gib(gpu_runner):
+    """B16 H32 Sq=Sk=32768: every tensor is 4 GiB, so the last (b, h) slices sit
+    past 2^32 bytes (64-bit row offsets, 32-bit buffer bounds per head)."""
+    import torch
+    b, h, s = 16, 32, 32768
+    q, k, v = _gpu_inputs(torch, b, h, s, s)
+    assert q.numel() * 2 == 1 << 32
+    _check_sampled(gpu_runner, torch, q, k, v, True, 0, with_lse=True, pairs=[(15, 31), (15, 0), (8, 17)],
+                   bar="north_star")
+    del q, k, v
+    torch.cuda.empty_cache()
