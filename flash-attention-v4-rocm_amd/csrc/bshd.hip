@@ -150,6 +150,36 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward(const Fa
     return causal ? dispatch<true>(*a, a->heads, config, stream) : dispatch<false>(*a, a->heads, config, stream);
 }
 
+// Packed variable-length sequences (no counterpart in the reference).
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_varlen(const Fav4VarlenArgs* a, int causal,
+                                                                       hipStream_t stream) {
+    if (!a || !a->q || !a->k || !a->v || !a->o || !a->cu_seqlens_q || !a->cu_seqlens_k || a->batch <= 0 ||
+        a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads != 0 || a->max_seqlen_q <= 0 ||
+        a->max_seqlen_k <= 0 || a->total_q <= 0 || a->total_k <= 0 || (causal != 0 && causal != 1) ||
+        !std::isfinite(a->scale) || a->scale <= 0)
+        return hipErrorInvalidValue;
+    if (a->batch > INT_MAX - 1 || a->heads > INT_MAX / 256 ||
+        int64_t(a->max_seqlen_q) * a->heads * 256 > int64_t(UINT32_MAX) ||
+        int64_t(a->max_seqlen_k) * a->kv_heads * 256 > int64_t(UINT32_MAX) ||
+        ((reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->k) |
+          reinterpret_cast<uintptr_t>(a->v) | reinterpret_cast<uintptr_t>(a->o)) & 15) ||
+        ((reinterpret_cast<uintptr_t>(a->cu_seqlens_q) | reinterpret_cast<uintptr_t>(a->cu_seqlens_k)) & 3) ||
+        (a->lse && (reinterpret_cast<uintptr_t>(a->lse) & 3)))
+        return hipErrorInvalidValue;
+    const int tiles = (a->max_seqlen_q + 255) / 256;
+    const int64_t total = int64_t(a->batch) * a->heads * tiles;
+    if (total > INT_MAX) return hipErrorInvalidValue;
+    const int grid = int(total < MAX_GRID ? total : MAX_GRID);
+    if (causal) {
+        if (a->lse) hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, true, true>), dim3(grid), dim3(512), 0, stream, *a, tiles, int(total));
+        else hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, true, false>), dim3(grid), dim3(512), 0, stream, *a, tiles, int(total));
+    } else {
+        if (a->lse) hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, false, true>), dim3(grid), dim3(512), 0, stream, *a, tiles, int(total));
+        else hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, false, false>), dim3(grid), dim3(512), 0, stream, *a, tiles, int(total));
+    }
+    return hipGetLastError();
+}
+
 // Grouped-query / multi-query attention (no counterpart in the reference).
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_gqa(const Fav4Args* a, int kv_heads,
                                                                     int causal, int config, hipStream_t stream) {

@@ -538,8 +538,10 @@ void fwd_kernel(Fav4Args a, int kv_heads, int tiles, int total) {
                 store8(ro, obase + (db * 32 + vg * 8) * 2, bf16x4{y0[0], y0[1], y1[0], y1[1]});
             }
         }
+        // An explicit FMA: every kernel rounds the LSE the same way, whatever
+        // the compiler's contraction choice in its surroundings.
         if constexpr (LSE) {
-            if (half == 0 && row < a.sq) a.lse[int64_t(bh) * a.sq + row] = st.m * LN2 + logf(st.l);
+            if (half == 0 && row < a.sq) a.lse[int64_t(bh) * a.sq + row] = __builtin_fmaf(st.m, LN2, logf(st.l));
         }
         wait_vmem();       // clamped prefetches have landed before the stages are reused
         __syncthreads();
@@ -709,6 +711,157 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
             float* lp = sp.lse_part + ((int64_t(split) * bhs + bh) * a.sq + row) * 2;
             lp[0] = st.m + __builtin_amdgcn_logf(st.lb);
             lp[1] = st.m + __builtin_amdgcn_logf(st.l);
+        }
+        wait_vmem();
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Varlen: packed sequences.  Q/O are [total_q, heads, 128] and K/V
+// [total_k, kv_heads, 128]; sequence b owns rows [cu_seqlens_q[b],
+// cu_seqlens_q[b+1]) and [cu_seqlens_k[b], cu_seqlens_k[b+1]); LSE is
+// [heads, total_q].  One item per (b, h, 256-row
+// q tile up to max_seqlen_q); items past a sequence's end do nothing.  The
+// offsets read from device memory are clamped to [0, total] and to the
+// maximum lengths, so every access stays inside the caller's buffers.
+// ---------------------------------------------------------------------------
+template <int BN, bool CAUSAL, bool LSE>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
+    constexpr int WAVES = 8, BM = 256;
+    constexpr int TILE_BYTES = BN * ROW_BYTES;
+    constexpr int STAGE_BYTES = 2 * TILE_BYTES;
+    constexpr int DMA = BN / 4 / WAVES;
+    static_assert(BN % 32 == 0 && BN % (4 * WAVES) == 0, "tile shape");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 31, half = lane >> 5;
+    const uint32_t row_bytes = uint32_t(a.heads) * ROW_BYTES;
+    const uint32_t kv_row_bytes = uint32_t(a.kv_heads) * ROW_BYTES;
+    const int group = a.heads / a.kv_heads;
+    const float scale2 = a.scale * LOG2E;
+    const uint32_t smem_base = lds_addr(smem);
+
+    LdsOffsets off;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) off.k[c] = col * ROW_BYTES + ((((2 * c) | half) ^ k_swz(col)) << 4);
+    {
+        const int r0 = half * 4 + ((lane & 15) >> 2);
+        const int gl = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r = r0 + 8 * j;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+                off.v[j][db] = r * ROW_BYTES + (((db * 4 + gl) ^ v_swz(r)) << 4) + ((lane & 1) << 3);
+        }
+    }
+    uint32_t dk[DMA], dv[DMA];
+#pragma unroll
+    for (int i = 0; i < DMA; ++i) {
+        const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
+        dk[i] = r * kv_row_bytes + ((p ^ k_swz(r)) << 4);
+        dv[i] = r * kv_row_bytes + ((p ^ v_swz(r)) << 4);
+    }
+
+    for (int id = blockIdx.x; id < total; id += gridDim.x) {
+        const int xcd = id & 7, slot = id >> 3, per = total >> 3, rem = total & 7;
+        const int logical = xcd * per + min(xcd, rem) + slot;
+        const int bh = __builtin_amdgcn_readfirstlane(logical / tiles);
+        const int tile = __builtin_amdgcn_readfirstlane(logical - bh * tiles);
+        const int batch = bh / a.heads, head = bh - batch * a.heads;
+        const int qs = min(max(__builtin_amdgcn_readfirstlane(a.cu_seqlens_q[batch]), 0), a.total_q);
+        const int qe = min(max(__builtin_amdgcn_readfirstlane(a.cu_seqlens_q[batch + 1]), qs), min(a.total_q, qs + a.max_seqlen_q));
+        const int ks = min(max(__builtin_amdgcn_readfirstlane(a.cu_seqlens_k[batch]), 0), a.total_k);
+        const int ke = min(max(__builtin_amdgcn_readfirstlane(a.cu_seqlens_k[batch + 1]), ks), min(a.total_k, ks + a.max_seqlen_k));
+        const int sq = qe - qs, sk = ke - ks;
+        const int q0 = tile * BM;
+        if (q0 >= sq) continue;    // uniform over the workgroup
+        const int qw = q0 + wave * 32, row = qw + col;
+        const int64_t qrow0 = (int64_t(qs) + q0) * a.heads + head;
+        const int64_t krow0 = int64_t(ks) * a.kv_heads + head / group;
+        const char* kbase = static_cast<const char*>(a.k) + krow0 * ROW_BYTES;
+        const char* vbase = static_cast<const char*>(a.v) + krow0 * ROW_BYTES;
+        const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + qrow0 * ROW_BYTES,
+                                    uint32_t(sq - q0 - 1) * row_bytes + ROW_BYTES);
+        const rsrc_t ro = make_rsrc(static_cast<char*>(a.o) + qrow0 * ROW_BYTES,
+                                    uint32_t(sq - q0 - 1) * row_bytes + ROW_BYTES);
+        const int kend = CAUSAL ? min(sk, q0 + BM) : sk;
+        const int ntiles = (kend + BN - 1) / BN;
+        const int nfull = (CAUSAL ? min(sk, q0 + 1) : sk) / BN;
+
+        RowState st;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) st.o[db] = f32x16{};
+        st.m = -__builtin_inff();
+        st.lb = 0.f;
+        st.l = 0.f;
+
+        if (ntiles > 0) {
+            auto issue = [&](int t) {
+                const int64_t first = int64_t(t) * BN;
+                const uint32_t bytes = uint32_t(sk - int(first) - 1) * kv_row_bytes + ROW_BYTES;
+                const u32x4 rk = make_desc(kbase + first * kv_row_bytes, bytes);
+                const u32x4 rv = make_desc(vbase + first * kv_row_bytes, bytes);
+                const uint32_t kd = smem_base + (t & 1) * STAGE_BYTES + wave * DMA * 1024;
+#pragma unroll
+                for (int i = 0; i < DMA; ++i) {
+                    dma16(rk, kd + i * 1024, dk[i]);
+                    dma16(rv, kd + TILE_BYTES + i * 1024, dv[i]);
+                }
+            };
+            issue(0);
+            bf16x8 qr[8];
+            {
+                const uint32_t qoff = uint32_t(wave * 32 + col) * row_bytes + half * 16;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) qr[c] = load16(rq, qoff + c * 32);
+#pragma unroll
+                for (int c = 0; c < 8; ++c) asm volatile("" ::"v"(qr[c]));
+            }
+            auto step = [&](auto stage_c, auto masked_c, int t) {
+                constexpr int STAGE = decltype(stage_c)::value;
+                const unsigned char* cur = smem + STAGE * STAGE_BYTES;
+                wait_vmem();
+                __syncthreads();
+                if (t + 1 < ntiles) issue(t + 1);
+                attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st, t == 0,
+                                                                       t * BN, sk, qw, row, half, scale2);
+            };
+            using S0 = std::integral_constant<int, 0>;
+            using S1 = std::integral_constant<int, 1>;
+            using Plain = std::integral_constant<bool, false>;
+            using Masked = std::integral_constant<bool, true>;
+            int t = 0;
+            for (; t + 1 < nfull; t += 2) {
+                step(S0{}, Plain{}, t);
+                step(S1{}, Plain{}, t + 1);
+            }
+            for (; t < ntiles; ++t) {
+                if (t & 1) step(S1{}, Masked{}, t);
+                else step(S0{}, Masked{}, t);
+            }
+        }
+
+        // O = acc / lb (0 for a sequence without keys), BF16.
+        const float inv = st.lb > 0.f ? 1.f / st.lb : 0.f;
+        const uint32_t obase = uint32_t(wave * 32 + col) * row_bytes + half * 8;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+#pragma unroll
+            for (int vg = 0; vg < 4; ++vg) {
+                const f32x2 x0 = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv};
+                const f32x2 x1 = {st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
+                const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
+                const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
+                store8(ro, obase + (db * 32 + vg * 8) * 2, bf16x4{y0[0], y0[1], y1[0], y1[1]});
+            }
+        }
+        if constexpr (LSE) {
+            if (half == 0 && row < sq) a.lse[int64_t(head) * a.total_q + qs + row] = __builtin_fmaf(st.m, LN2, logf(st.l));
         }
         wait_vmem();
         __syncthreads();

@@ -37,6 +37,13 @@ class Args(C.Structure):
         (n, C.c_int) for n in ("batch", "heads", "sq", "sk")] + [("scale", C.c_float)]
 
 
+class VarlenArgs(C.Structure):
+    """``struct Fav4VarlenArgs`` (include/fav4_bshd.h): 7 pointers, 7 ints, 1 float."""
+    _fields_ = [(n, C.c_void_p) for n in ("q", "k", "v", "o", "lse", "cu_seqlens_q", "cu_seqlens_k")] + [
+        (n, C.c_int) for n in ("batch", "heads", "kv_heads", "max_seqlen_q", "max_seqlen_k", "total_q",
+                               "total_k")] + [("scale", C.c_float)]
+
+
 def build_library(out: Path = LIB_PATH, verbose: bool = False) -> Path:
     """Compile ``csrc/bshd.hip`` for gfx950 into ``build/libfav4_bshd.so``."""
     out.parent.mkdir(parents=True, exist_ok=True)
@@ -75,6 +82,8 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
         lib.fav4_bshd_splitkv_select.restype = C.c_int
         lib.fav4_bshd_forward_gqa.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_int, C.c_void_p]
         lib.fav4_bshd_forward_gqa.restype = C.c_int
+        lib.fav4_bshd_forward_varlen.argtypes = [C.POINTER(VarlenArgs), C.c_int, C.c_void_p]
+        lib.fav4_bshd_forward_varlen.restype = C.c_int
         _LIB = lib
     return _LIB
 
@@ -152,6 +161,31 @@ class Runner:
         if status:
             raise RuntimeError(f"splitkv splits {splits}: HIP status {status}")
         return workspace
+
+    # ---- packed variable-length sequences (fav4_bshd_forward_varlen; no reference counterpart) ----
+    def varlen_args(self, q, k, v, o, lse, cu_q, cu_k, max_q, max_k, scale=None) -> VarlenArgs:
+        """q/o: [total_q, heads, 128]; k/v: [total_k, kv_heads, 128] (BF16, contiguous);
+        cu_q/cu_k: int32 [batch+1] on the device; lse: FP32 [heads, total_q] or None."""
+        import torch
+        assert all(x.dtype == torch.bfloat16 and x.is_cuda and x.is_contiguous() for x in (q, k, v, o))
+        assert q.dim() == 3 and q.shape[2] == D and o.shape == q.shape and k.shape == v.shape and k.dim() == 3
+        assert all(c.dtype == torch.int32 and c.is_cuda and c.is_contiguous() and c.dim() == 1 for c in (cu_q, cu_k))
+        assert cu_q.numel() == cu_k.numel() >= 2
+        tq, h, _ = q.shape
+        assert lse is None or (tuple(lse.shape) == (h, tq) and lse.is_contiguous() and lse.dtype == torch.float32)
+        return VarlenArgs(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                          lse.data_ptr() if lse is not None else None, cu_q.data_ptr(), cu_k.data_ptr(),
+                          cu_q.numel() - 1, h, k.shape[1], int(max_q), int(max_k), tq, k.shape[0],
+                          1 / math.sqrt(D) if scale is None else scale)
+
+    def call_varlen(self, q, k, v, o, lse, cu_q, cu_k, max_q, max_k, causal, scale=None, stream=None):
+        import torch
+        a = self.varlen_args(q, k, v, o, lse, cu_q, cu_k, max_q, max_k, scale)
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
+        status = self.hip.fav4_bshd_forward_varlen(C.byref(a), int(causal), stream)
+        if status:
+            raise RuntimeError(f"varlen: HIP status {status}")
 
 
 def forward(q, k, v, causal=False, with_lse=False, config=0, scale=None):

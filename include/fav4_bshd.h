@@ -74,3 +74,31 @@ extern "C" int fav4_bshd_splitkv_select(const Fav4Args* args, int causal);
 // kv_heads > heads or heads % kv_heads != 0.
 extern "C" int fav4_bshd_forward_gqa(const Fav4Args* args, int kv_heads, int causal, int config,
                                      hipStream_t stream);
+
+// ---- Variable-length (packed) sequences ---------------------------------------
+// No counterpart in the reference.  `batch` sequences are packed along the
+// row axis: sequence b's queries are rows [cu_seqlens_q[b], cu_seqlens_q[b+1])
+// of Q/O and its keys rows [cu_seqlens_k[b], cu_seqlens_k[b+1]) of K/V; each
+// sequence is attended on its own (top-left causal within the sequence when
+// causal = 1), exactly as fav4_bshd_forward would on that sequence alone
+// (bitwise, for sequences of at least one key).  A sequence with no keys gets
+// O = 0 and LSE = -inf.  GQA as in fav4_bshd_forward_gqa.
+struct Fav4VarlenArgs {
+    const void *q, *k, *v;             // BF16 [total_q | total_k, heads | kv_heads, 128], contiguous
+    void *o;                           // BF16 [total_q, heads, 128], contiguous
+    float *lse;                        // optional FP32 [heads, total_q]; NULL = not written
+    const int *cu_seqlens_q;           // device int32 [batch + 1], non-decreasing from 0
+    const int *cu_seqlens_k;           // device int32 [batch + 1], non-decreasing from 0
+    int batch, heads, kv_heads;        // kv_heads divides heads
+    int max_seqlen_q, max_seqlen_k;    // bounds of every sequence's length
+    int total_q, total_k;              // rows of Q/O and of K/V
+    float scale;
+};
+// The offsets are read on the device and clamped to [0, total] and to the
+// maximum lengths (so malformed offsets cannot move an access outside the
+// buffers; they do give undefined results).  Returns 0, hipErrorInvalidValue
+// (1) for rejected arguments (checked before any HIP call: NULL pointers,
+// sizes < 1, kv_heads not dividing heads, bad causal / scale, misalignment,
+// max_seqlen * heads * 256 >= 2^32), else the launch status.  Allocates
+// nothing and never synchronizes.
+extern "C" int fav4_bshd_forward_varlen(const Fav4VarlenArgs* args, int causal, hipStream_t stream);

@@ -1,7 +1,7 @@
 """Host-only checks of the C ABI (no GPU needed, no compute call is made).
 
 The library must export the two entry points of the reference header
-(include/fav4_bshd.h:19-20) plus the three split-KV ones of this build, lay
+(include/fav4_bshd.h:19-20) plus this build's split-KV, GQA and varlen ones, lay
 out Fav4Args byte for byte like the reference (include/fav4_bshd.h:4-10), and
 reject bad arguments with hipErrorInvalidValue before touching HIP, as
 src/bshd.hip:27-34 does.  The split-KV size / plan queries are checked
@@ -46,7 +46,8 @@ def test_exports_exactly_the_c_abi():
     names = {line.split()[-1] for line in out.splitlines() if line.strip()}
     public = {n for n in names if not n.startswith("_")}
     assert public == {"fav4_bshd_forward", "fav4_bshd_select_config", "fav4_bshd_forward_splitkv",
-                      "fav4_bshd_splitkv_workspace_size", "fav4_bshd_splitkv_select", "fav4_bshd_forward_gqa"}, public
+                      "fav4_bshd_splitkv_workspace_size", "fav4_bshd_splitkv_select", "fav4_bshd_forward_gqa",
+                      "fav4_bshd_forward_varlen"}, public
 
 
 def test_ctypes_layout_matches_reference(Args):
@@ -209,3 +210,63 @@ def test_gqa_rejects_bad_kv_heads(lib, Args, kv_heads):
     assert lib.fav4_bshd_forward_gqa(C.byref(a), kv_heads, 0, 0, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fav4_bshd_forward_gqa(C.byref(a), 2, 2, 0, None) == HIP_ERROR_INVALID_VALUE   # bad causal
     assert lib.fav4_bshd_forward_gqa(None, 2, 0, 0, None) == HIP_ERROR_INVALID_VALUE
+
+
+# ---- packed variable-length sequences --------------------------------------
+VLAYOUT = dict(q=0, k=8, v=16, o=24, lse=32, cu_seqlens_q=40, cu_seqlens_k=48, batch=56, heads=60, kv_heads=64,
+               max_seqlen_q=68, max_seqlen_k=72, total_q=76, total_k=80, scale=84)
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_varlen_layout_ctypes_and_header(tmp_path):
+    VarlenArgs = load_package().VarlenArgs
+    assert C.sizeof(VarlenArgs) == 88
+    for name, offset in VLAYOUT.items():
+        assert getattr(VarlenArgs, name).offset == offset, name
+    src = tmp_path / "vlayout.cpp"
+    fields = ", ".join(f'offsetof(Fav4VarlenArgs, {n})' for n in VLAYOUT)
+    src.write_text(
+        '#include <cstddef>\n#include <cstdio>\n#include "fav4_bshd.h"\n'
+        'int main() { size_t o[] = {' + fields + '};\n'
+        '  std::printf("%zu", sizeof(Fav4VarlenArgs)); for (size_t x : o) std::printf(" %zu", x); }\n')
+    exe = tmp_path / "vlayout"
+    subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", f"-I{HEADER.parent}", "-I/opt/rocm/include",
+                    str(src), "-o", str(exe)], check=True, capture_output=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got == [88] + list(VLAYOUT.values())
+
+
+def _vgood():
+    return dict(q=0x10000, k=0x20000, v=0x30000, o=0x40000, lse=None, cu_seqlens_q=0x50000, cu_seqlens_k=0x60000,
+                batch=3, heads=4, kv_heads=2, max_seqlen_q=300, max_seqlen_k=500, total_q=600, total_k=900,
+                scale=1 / math.sqrt(128))
+
+
+VBAD = [
+    ("q_null", dict(q=None)), ("k_null", dict(k=None)), ("v_null", dict(v=None)), ("o_null", dict(o=None)),
+    ("cuq_null", dict(cu_seqlens_q=None)), ("cuk_null", dict(cu_seqlens_k=None)),
+    ("batch0", dict(batch=0)), ("heads0", dict(heads=0)), ("kv0", dict(kv_heads=0)), ("kv3", dict(kv_heads=3)),
+    ("kv8", dict(kv_heads=8)), ("maxq0", dict(max_seqlen_q=0)), ("maxk0", dict(max_seqlen_k=0)),
+    ("totq0", dict(total_q=0)), ("totk_neg", dict(total_k=-5)),
+    ("scale0", dict(scale=0.0)), ("scale_nan", dict(scale=float("nan"))), ("scale_inf", dict(scale=float("inf"))),
+    ("q_overflow", dict(max_seqlen_q=1 << 22)), ("k_overflow", dict(kv_heads=4, max_seqlen_k=1 << 22)),
+    ("q_misaligned", dict(q=0x10008)), ("o_misaligned", dict(o=0x40002)), ("cu_misaligned", dict(cu_seqlens_k=0x60002)),
+    ("lse_misaligned", dict(lse=0x70001)),
+    ("grid_overflow", dict(batch=1 << 20, heads=1 << 10, kv_heads=1, max_seqlen_q=1 << 10)),
+]
+
+
+@pytest.mark.parametrize("name,change", VBAD, ids=[b[0] for b in VBAD])
+def test_varlen_rejects_bad_arguments(lib, name, change):
+    VarlenArgs = load_package().VarlenArgs
+    f = _vgood()
+    f.update(change)
+    a = VarlenArgs(**f)
+    assert lib.fav4_bshd_forward_varlen(C.byref(a), 0, None) == HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.parametrize("causal", [-1, 2])
+def test_varlen_rejects_bad_causal(lib, causal):
+    a = load_package().VarlenArgs(**_vgood())
+    assert lib.fav4_bshd_forward_varlen(C.byref(a), causal, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_forward_varlen(None, 0, None) == HIP_ERROR_INVALID_VALUE
