@@ -62,6 +62,7 @@ def parse_args():
     p.add_argument("--sweep", default="", help="comma list of extra sequence lengths to time (report only)")
     p.add_argument("--no-comparator", action="store_true", help="skip the torch SDPA comparator")
     p.add_argument("--no-splitkv", action="store_true", help="skip the split-KV report (B1 H8 Sq1024 Sk32768)")
+    p.add_argument("--no-api", action="store_true", help="skip the GQA / varlen report")
     p.add_argument("--no-telemetry", action="store_true",
                    help="start no child processes (amd-smi clocks, hipcc version), e.g. under a profiler")
     p.add_argument("--pmc-pass", action="store_true",
@@ -252,6 +253,7 @@ def splitkv_report(torch, orc, runner, args, stream, b=1, h=8, sq=1024, sk=32768
         res = {"splits": splits, "workspace_bytes": ws.numel()}
         for name, fn in (("plain", plain), ("splitkv", split)):
             o.fill_(float("nan"))
+            torch.cuda.synchronize()   # the fill runs on the default stream
             with torch.cuda.stream(stream):
                 fn()
             torch.cuda.synchronize()
@@ -266,6 +268,63 @@ def splitkv_report(torch, orc, runner, args, stream, b=1, h=8, sq=1024, sk=32768
               f"split-KV ({splits} chunks) {res['splitkv']['tflops']} TFLOP/s, x{res['speedup']}",
               file=sys.stderr, flush=True)
         del ws
+    del q, k, v, o
+    torch.cuda.empty_cache()
+    return out
+
+
+def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
+    """The GQA and varlen entry points at the headline token count (B*S rows, H8):
+    GQA with `kvh` K/V heads; varlen with B ragged sequences of seeded lengths in
+    [S/4, 7S/4].  Graph-timed, each output first checked against the FP64 oracle
+    on sampled rows of two (sequence, head) pairs of two sequences."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11939)
+    mk = lambda *shape: torch.randn(shape, device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
+    out = {}
+
+    def measure(name, fn, o, checks, flop):
+        o.fill_(float("nan"))
+        torch.cuda.synchronize()   # the fill runs on the default stream
+        with torch.cuda.stream(stream):
+            fn()
+        torch.cuda.synchronize()
+        for qc, kc, vc, oc, causal in checks():
+            err, _ = check_rows(torch, orc, qc, kc, vc, oc, causal, [(0, 0), (0, h - 1)])
+            if not orc.check_north_star_tolerance(err):
+                raise SystemExit(f"api report: {name} check failed: {err}")
+        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream))
+        print(f"# {name}: {us:.1f} us, {flop / us / 1e6:.1f} TFLOP/s", file=sys.stderr, flush=True)
+        return dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1))
+
+    q, k, v = mk(b, s, h, 128), mk(b, s, kvh, 128), mk(b, s, kvh, 128)
+    o = torch.empty_like(q)
+    grp = h // kvh
+    res = {"workload": f"B{b} H{h} KV heads {kvh} Sq=Sk={s} D128 BF16, LSE off"}
+    for causal in (False, True):
+        fn = lambda: runner.call_gqa(q, k, v, o, None, causal, 0, stream=stream.cuda_stream)
+        checks = lambda: [(q[i:i + 1], k[i:i + 1].repeat_interleave(grp, dim=2),
+                           v[i:i + 1].repeat_interleave(grp, dim=2), o[i:i + 1], causal) for i in (0, b - 1)]
+        res["causal" if causal else "dense"] = measure(f"gqa causal={causal}", fn, o, checks,
+                                                       orc.flops(b, h, s, s, causal))
+    out["gqa"] = res
+    del q, k, v, o
+
+    lens = np.random.default_rng(11939).integers(s // 4, 7 * s // 4 + 1, size=b)
+    cu_h = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    total, maxlen = int(cu_h[-1]), int(lens.max())
+    cu = torch.from_numpy(cu_h).cuda()
+    q, k, v = mk(total, h, 128), mk(total, h, 128), mk(total, h, 128)
+    o = torch.empty_like(q)
+    res = {"workload": f"{b} sequences, lengths {int(lens.min())}..{maxlen} (seeded), {total} tokens, "
+                       f"H{h} D128 BF16, LSE off"}
+    for causal in (False, True):
+        fn = lambda: runner.call_varlen(q, k, v, o, None, cu, cu, maxlen, maxlen, causal, stream=stream.cuda_stream)
+        sel = (0, int(np.argmax(lens)))
+        checks = lambda: [tuple(x[cu_h[i]:cu_h[i + 1]][None] for x in (q, k, v, o)) + (causal,) for i in sel]
+        flop = sum(orc.flops(1, h, int(n), int(n), causal) for n in lens)
+        res["causal" if causal else "dense"] = measure(f"varlen causal={causal}", fn, o, checks, flop)
+    out["varlen"] = res
     del q, k, v, o
     torch.cuda.empty_cache()
     return out
@@ -381,6 +440,7 @@ def main():
         check = None
         if not args.no_check:
             o.fill_(float("nan"))
+            torch.cuda.synchronize()   # the fill runs on the default stream
             with torch.cuda.stream(stream):
                 fn()
             torch.cuda.synchronize()
@@ -400,6 +460,7 @@ def main():
     if not args.no_comparator:
         cmp = comparator(torch, orc, runner, q, k, v, o, stream, args, list(results))
     skv = None if args.no_splitkv else splitkv_report(torch, orc, runner, args, stream)
+    api = None if args.no_api else api_report(torch, orc, runner, args, stream)
 
     sweep = {}
     for n in [int(x) for x in args.sweep.split(",") if x]:
@@ -459,6 +520,7 @@ def main():
     line["dense_samples_us"] = [round(x, 2) for x in dense["samples_us"]]
     line["comparator"] = cmp
     line["splitkv"] = skv
+    line["api"] = api
     prov["clocks_after"] = gpu_clocks()
     line["provenance"] = prov
     if sweep:

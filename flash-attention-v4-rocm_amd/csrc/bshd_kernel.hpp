@@ -767,11 +767,29 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
         dv[i] = r * kv_row_bytes + ((p ^ v_swz(r)) << 4);
     }
 
+    // Item order.  Each XCD gets a contiguous run of logical items (all q
+    // tiles of a (sequence, head) together, for its L2), but the runs are cut
+    // from the (sequence, head) pairs taken column by column from an 8-wide
+    // grid, bh = 8*row + col: XCD x holds mostly the pairs with bh % 8 == x,
+    // i.e. a share of every sequence rather than a few whole sequences, so
+    // ragged lengths do not leave XCDs idle.  Within a pair the q tiles run
+    // last-to-first (causal: heaviest first).
+    const int nbh = a.batch * a.heads, full = nbh >> 3, rem8 = nbh & 7;
     for (int id = blockIdx.x; id < total; id += gridDim.x) {
         const int xcd = id & 7, slot = id >> 3, per = total >> 3, rem = total & 7;
         const int logical = xcd * per + min(xcd, rem) + slot;
-        const int bh = __builtin_amdgcn_readfirstlane(logical / tiles);
-        const int tile = __builtin_amdgcn_readfirstlane(logical - bh * tiles);
+        const int j = __builtin_amdgcn_readfirstlane(logical / tiles);
+        const int tile = __builtin_amdgcn_readfirstlane(tiles - 1 - (logical - j * tiles));
+        int gcol, grow;
+        if (j < rem8 * (full + 1)) {
+            gcol = j / (full + 1);
+            grow = j - gcol * (full + 1);
+        } else {
+            const int jj = j - rem8 * (full + 1);
+            gcol = rem8 + jj / full;
+            grow = jj - (gcol - rem8) * full;
+        }
+        const int bh = grow * 8 + gcol;
         const int batch = bh / a.heads, head = bh - batch * a.heads;
         const int qs = min(max(__builtin_amdgcn_readfirstlane(a.cu_seqlens_q[batch]), 0), a.total_q);
         const int qe = min(max(__builtin_amdgcn_readfirstlane(a.cu_seqlens_q[batch + 1]), qs), min(a.total_q, qs + a.max_seqlen_q));
