@@ -17,7 +17,7 @@ namespace {
 constexpr int64_t MAX_GRID = int64_t(1) << 22;
 
 template <int WAVES, int BN, int STAGES, bool PIPE, bool CAUSAL>
-int launch(const Fav4Args& a, int kv_heads, hipStream_t stream) {
+int launch(const Fav4Args& a, const fav4::Layout& L, hipStream_t stream) {
     constexpr int BM = WAVES * 32;
     const int tiles = (a.sq + BM - 1) / BM;
     const int64_t total = int64_t(fav4::items_per_head<CAUSAL>(tiles)) * a.batch * a.heads;
@@ -25,19 +25,19 @@ int launch(const Fav4Args& a, int kv_heads, hipStream_t stream) {
     const int grid = int(total < MAX_GRID ? total : MAX_GRID);
     if (a.lse)
         hipLaunchKernelGGL((fav4::fwd_kernel<WAVES, BN, CAUSAL, true, STAGES, PIPE>), dim3(grid),
-                           dim3(WAVES * 64), 0, stream, a, kv_heads, tiles, int(total));
+                           dim3(WAVES * 64), 0, stream, a, L, tiles, int(total));
     else
         hipLaunchKernelGGL((fav4::fwd_kernel<WAVES, BN, CAUSAL, false, STAGES, PIPE>), dim3(grid),
-                           dim3(WAVES * 64), 0, stream, a, kv_heads, tiles, int(total));
+                           dim3(WAVES * 64), 0, stream, a, L, tiles, int(total));
     return hipGetLastError();
 }
 
 template <bool CAUSAL>
-int dispatch(const Fav4Args& a, int kv_heads, int config, hipStream_t stream) {
+int dispatch(const Fav4Args& a, const fav4::Layout& L, int config, hipStream_t stream) {
     switch (config) {
-    case 1: return launch<4, 64, 2, false, CAUSAL>(a, kv_heads, stream);
-    case 2: return launch<8, 64, 2, false, CAUSAL>(a, kv_heads, stream);
-    case 3: return launch<8, 64, 3, true, CAUSAL>(a, kv_heads, stream);
+    case 1: return launch<4, 64, 2, false, CAUSAL>(a, L, stream);
+    case 2: return launch<8, 64, 2, false, CAUSAL>(a, L, stream);
+    case 3: return launch<8, 64, 3, true, CAUSAL>(a, L, stream);
     default: return hipErrorInvalidValue;
     }
 }
@@ -54,6 +54,33 @@ int validate(const Fav4Args* a, int causal, int config) {
           reinterpret_cast<uintptr_t>(a->v) | reinterpret_cast<uintptr_t>(a->o)) & 15))
         return hipErrorInvalidValue;
     return hipSuccess;
+}
+
+// Contiguous BSHD Q/O [B, Sq, H, 128] and K/V [B, Sk, kv_heads, 128].
+fav4::Layout bshd_layout(const Fav4Args& a, int kv_heads) {
+    fav4::Layout L;
+    const int64_t row = int64_t(a.heads) * fav4::ROW_BYTES, kvrow = int64_t(kv_heads) * fav4::ROW_BYTES;
+    L.qr = L.orow = uint32_t(row);
+    L.kr = L.vr = uint32_t(kvrow);
+    L.qb = L.ob = row * a.sq;
+    L.kb = L.vb = kvrow * a.sk;
+    L.qh = L.oh = L.kh = L.vh = fav4::ROW_BYTES;
+    L.group = a.heads / kv_heads;
+    return L;
+}
+
+// One tensor's element strides, checked: non-negative, multiples of 8
+// elements (every row starts 16-byte aligned), the rows of one (batch, head)
+// slice within a 4 GiB buffer bound, and the whole view within 2^48 bytes (so
+// no address computation can overflow).
+bool stride_ok(const Fav4Strides* st, int batch, int heads, int rows) {
+    if (!st || st->batch < 0 || st->seq <= 0 || st->head < 0 || ((st->batch | st->seq | st->head) & 7))
+        return false;
+    if ((int64_t(rows) - 1) * static_cast<__int128>(st->seq) * 2 + fav4::ROW_BYTES > int64_t(UINT32_MAX))
+        return false;
+    const __int128 span = static_cast<__int128>(batch - 1) * st->batch + static_cast<__int128>(heads - 1) * st->head +
+                          static_cast<__int128>(rows - 1) * st->seq + fav4::D;
+    return span * 2 <= (static_cast<__int128>(1) << 48);
 }
 
 // ---- split-KV -------------------------------------------------------------
@@ -147,7 +174,31 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward(const Fa
     const int st = validate(a, causal, config);
     if (st != hipSuccess) return st;
     if (config == 0) config = fav4_bshd_select_config(a);
-    return causal ? dispatch<true>(*a, a->heads, config, stream) : dispatch<false>(*a, a->heads, config, stream);
+    const fav4::Layout L = bshd_layout(*a, a->heads);
+    return causal ? dispatch<true>(*a, L, config, stream) : dispatch<false>(*a, L, config, stream);
+}
+
+// Arbitrary strides (no counterpart in the reference).
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_strided(
+    const Fav4Args* a, int kv_heads, const Fav4Strides* q, const Fav4Strides* k, const Fav4Strides* v,
+    const Fav4Strides* o, int causal, int config, hipStream_t stream) {
+    if (!a || !a->q || !a->k || !a->v || !a->o || a->batch <= 0 || a->heads <= 0 || a->sq <= 0 || a->sk <= 0 ||
+        (causal != 0 && causal != 1) || config < 0 || config > 3 || !std::isfinite(a->scale) || a->scale <= 0 ||
+        kv_heads <= 0 || kv_heads > a->heads || a->heads % kv_heads != 0 || a->batch > INT_MAX / a->heads ||
+        ((reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->k) |
+          reinterpret_cast<uintptr_t>(a->v) | reinterpret_cast<uintptr_t>(a->o)) & 15) ||
+        (a->lse && (reinterpret_cast<uintptr_t>(a->lse) & 3)) ||
+        !stride_ok(q, a->batch, a->heads, a->sq) || !stride_ok(o, a->batch, a->heads, a->sq) ||
+        !stride_ok(k, a->batch, kv_heads, a->sk) || !stride_ok(v, a->batch, kv_heads, a->sk))
+        return hipErrorInvalidValue;
+    fav4::Layout L;
+    L.qb = q->batch * 2; L.qh = q->head * 2; L.qr = uint32_t(q->seq * 2);
+    L.kb = k->batch * 2; L.kh = k->head * 2; L.kr = uint32_t(k->seq * 2);
+    L.vb = v->batch * 2; L.vh = v->head * 2; L.vr = uint32_t(v->seq * 2);
+    L.ob = o->batch * 2; L.oh = o->head * 2; L.orow = uint32_t(o->seq * 2);
+    L.group = a->heads / kv_heads;
+    if (config == 0) config = fav4_bshd_select_config(a);
+    return causal ? dispatch<true>(*a, L, config, stream) : dispatch<false>(*a, L, config, stream);
 }
 
 // Packed variable-length sequences (no counterpart in the reference).
@@ -187,7 +238,8 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_gqa(cons
     if (st != hipSuccess) return st;
     if (kv_heads <= 0 || kv_heads > a->heads || a->heads % kv_heads != 0) return hipErrorInvalidValue;
     if (config == 0) config = fav4_bshd_select_config(a);
-    return causal ? dispatch<true>(*a, kv_heads, config, stream) : dispatch<false>(*a, kv_heads, config, stream);
+    const fav4::Layout L = bshd_layout(*a, kv_heads);
+    return causal ? dispatch<true>(*a, L, config, stream) : dispatch<false>(*a, L, config, stream);
 }
 
 // Split-KV entry points (no counterpart in the reference; see the header).

@@ -69,6 +69,15 @@ __device__ __forceinline__ void for_each_item(int tiles, int total, F&& process)
     }
 }
 
+// Byte strides of Q, K, V and O seen as [B, S, H, 128] (the 128 head dims
+// contiguous).  Row = one sequence position of one head.  BSHD: row stride
+// heads*256 (K/V: kv_heads*256), batch stride S*row, head stride 256.
+struct Layout {
+    int64_t qb, qh, kb, kh, vb, vh, ob, oh;   // batch / head strides
+    uint32_t qr, kr, vr, orow;                // row strides (each slice's rows fit a 4 GiB buffer bound)
+    int group;                                // query heads per K/V head
+};
+
 // Per-wave running state of the online softmax for its 32 query rows.
 // m: base in log2 units (identical in both lane halves); lb: sum of the BF16
 // weights that entered the PV product; l: FP32 sum (only kept for the LSE).
@@ -309,7 +318,7 @@ __device__ __forceinline__ void pv_plain(const unsigned char* vs, const LdsOffse
 // stage.  Masked tiles (causal diagonal, key tail) follow unpipelined.
 template <int WAVES, int BN, bool CAUSAL, bool LSE, int STAGES, bool PIPE = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void fwd_kernel(Fav4Args a, int kv_heads, int tiles, int total) {
+void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
     static_assert(!PIPE || STAGES == 3, "the cross-tile pipeline keeps three tiles in LDS");
     constexpr int BM = WAVES * 32;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
@@ -323,9 +332,6 @@ void fwd_kernel(Fav4Args a, int kv_heads, int tiles, int total) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 31, half = lane >> 5;
-    const uint32_t row_bytes = uint32_t(a.heads) * ROW_BYTES;   // Q/O stride between sequence positions
-    const uint32_t kv_row_bytes = uint32_t(kv_heads) * ROW_BYTES;   // K/V stride (kv_heads divides heads)
-    const int group = a.heads / kv_heads;                           // query heads per K/V head
     const float scale2 = a.scale * LOG2E;
     const uint32_t smem_base = lds_addr(smem);
 
@@ -348,22 +354,21 @@ void fwd_kernel(Fav4Args a, int kv_heads, int tiles, int total) {
 #pragma unroll
     for (int i = 0; i < DMA; ++i) {
         const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
-        dk[i] = r * kv_row_bytes + ((p ^ k_swz(r)) << 4);
-        dv[i] = r * kv_row_bytes + ((p ^ v_swz(r)) << 4);
+        dk[i] = r * L.kr + ((p ^ k_swz(r)) << 4);
+        dv[i] = r * L.vr + ((p ^ v_swz(r)) << 4);
     }
 
     auto process = [&](int bh, int tile) {
         const int batch = bh / a.heads, head = bh - batch * a.heads;
         const int q0 = tile * BM, qw = q0 + wave * 32;
         const int row = qw + col;                                 // this lane's query row
-        const int64_t qrow0 = (int64_t(batch) * a.sq + q0) * a.heads + head;
-        const int64_t krow0 = int64_t(batch) * a.sk * kv_heads + head / group;
-        const char* kbase = static_cast<const char*>(a.k) + krow0 * ROW_BYTES;
-        const char* vbase = static_cast<const char*>(a.v) + krow0 * ROW_BYTES;
-        const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + qrow0 * ROW_BYTES,
-                                    uint32_t(a.sq - q0 - 1) * row_bytes + ROW_BYTES);
-        const rsrc_t ro = make_rsrc(static_cast<char*>(a.o) + qrow0 * ROW_BYTES,
-                                    uint32_t(a.sq - q0 - 1) * row_bytes + ROW_BYTES);
+        const int kvh = head / L.group;
+        const char* kbase = static_cast<const char*>(a.k) + batch * L.kb + kvh * L.kh;
+        const char* vbase = static_cast<const char*>(a.v) + batch * L.vb + kvh * L.vh;
+        const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + batch * L.qb + head * L.qh + int64_t(q0) * L.qr,
+                                    uint32_t(a.sq - q0 - 1) * L.qr + ROW_BYTES);
+        const rsrc_t ro = make_rsrc(static_cast<char*>(a.o) + batch * L.ob + head * L.oh + int64_t(q0) * L.orow,
+                                    uint32_t(a.sq - q0 - 1) * L.orow + ROW_BYTES);
         // Key tiles: [0, nfull) are unmasked for every row of the workgroup,
         // [nfull, ntiles) cross the key tail or the causal diagonal.
         constexpr int BNT = BN;                           // keys per LDS tile
@@ -377,9 +382,9 @@ void fwd_kernel(Fav4Args a, int kv_heads, int tiles, int total) {
         auto issue = [&](int t) {
             const int tc = min(t, ntiles - 1);
             const int64_t first = int64_t(tc) * BNT;
-            const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * kv_row_bytes + ROW_BYTES;
-            const u32x4 rk = make_desc(kbase + first * kv_row_bytes, bytes);
-            const u32x4 rv = make_desc(vbase + first * kv_row_bytes, bytes);
+            const uint32_t rows = uint32_t(a.sk - int(first) - 1);
+            const u32x4 rk = make_desc(kbase + first * L.kr, rows * L.kr + ROW_BYTES);
+            const u32x4 rv = make_desc(vbase + first * L.vr, rows * L.vr + ROW_BYTES);
             const uint32_t ks = smem_base + (t % STAGES) * STAGE_BYTES + wave * DMA * 1024;
 #pragma unroll
             for (int i = 0; i < DMA; ++i) {
@@ -392,7 +397,7 @@ void fwd_kernel(Fav4Args a, int kv_heads, int tiles, int total) {
         for (int t = 0; t < AHEAD; ++t) issue(t);   // PIPE: tiles 0 and 1
         bf16x8 qr[8];
         {
-            const uint32_t qoff = uint32_t(wave * 32 + col) * row_bytes + half * 16;
+            const uint32_t qoff = uint32_t(wave * 32 + col) * L.qr + half * 16;
 #pragma unroll
             for (int c = 0; c < 8; ++c) qr[c] = load16(rq, qoff + c * 32);
             // Retire the Q loads here, so that inside the key loop the only
@@ -526,7 +531,7 @@ void fwd_kernel(Fav4Args a, int kv_heads, int tiles, int total) {
         // the BF16 rounding of P perturbs O by sum_j w_j e_j (V_j - O) instead
         // of sum_j w_j e_j V_j (exact when one key dominates).
         const float inv = 1.f / st.lb;
-        const uint32_t obase = uint32_t(wave * 32 + col) * row_bytes + half * 8;
+        const uint32_t obase = uint32_t(wave * 32 + col) * L.orow + half * 8;
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
 #pragma unroll

@@ -44,6 +44,11 @@ class VarlenArgs(C.Structure):
                                "total_k")] + [("scale", C.c_float)]
 
 
+class Strides(C.Structure):
+    """``struct Fav4Strides`` (include/fav4_bshd.h): element strides of a [B, S, H, 128] view."""
+    _fields_ = [(n, C.c_longlong) for n in ("batch", "seq", "head")]
+
+
 def build_library(out: Path = LIB_PATH, verbose: bool = False) -> Path:
     """Compile ``csrc/bshd.hip`` for gfx950 into ``build/libfav4_bshd.so``."""
     out.parent.mkdir(parents=True, exist_ok=True)
@@ -82,6 +87,9 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
         lib.fav4_bshd_splitkv_select.restype = C.c_int
         lib.fav4_bshd_forward_gqa.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_int, C.c_void_p]
         lib.fav4_bshd_forward_gqa.restype = C.c_int
+        lib.fav4_bshd_forward_strided.argtypes = [C.POINTER(Args), C.c_int] + [C.POINTER(Strides)] * 4 + [
+            C.c_int, C.c_int, C.c_void_p]
+        lib.fav4_bshd_forward_strided.restype = C.c_int
         lib.fav4_bshd_forward_varlen.argtypes = [C.POINTER(VarlenArgs), C.c_int, C.c_void_p]
         lib.fav4_bshd_forward_varlen.restype = C.c_int
         _LIB = lib
@@ -161,6 +169,28 @@ class Runner:
         if status:
             raise RuntimeError(f"splitkv splits {splits}: HIP status {status}")
         return workspace
+
+    # ---- arbitrary strides (fav4_bshd_forward_strided; no reference counterpart) ----
+    def call_strided(self, q, k, v, o, lse, causal, config=0, scale=None, stream=None):
+        """q/o: [B, Sq, H, 128] and k/v: [B, Sk, KVH, 128] views with any strides whose last
+        dimension is contiguous (e.g. ``x_bhsd.transpose(1, 2)``, ``qkv[:, :, 0]``);
+        lse: FP32 [B, H, Sq] contiguous or None."""
+        import torch
+        for x in (q, k, v, o):
+            assert x.dtype == torch.bfloat16 and x.is_cuda and x.dim() == 4 and x.shape[3] == D and x.stride(3) == 1
+        b, sq, h, _ = q.shape
+        assert o.shape == q.shape and k.shape == v.shape and k.shape[0] == b
+        assert lse is None or (tuple(lse.shape) == (b, h, sq) and lse.is_contiguous() and lse.dtype == torch.float32)
+        a = Args(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                 lse.data_ptr() if lse is not None else None, b, h, sq, k.shape[1],
+                 1 / math.sqrt(D) if scale is None else scale)
+        st = [Strides(x.stride(0), x.stride(1), x.stride(2)) for x in (q, k, v, o)]
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
+        status = self.hip.fav4_bshd_forward_strided(C.byref(a), int(k.shape[2]), *[C.byref(x) for x in st],
+                                                    int(causal), int(config), stream)
+        if status:
+            raise RuntimeError(f"strided config {config}: HIP status {status}")
 
     # ---- packed variable-length sequences (fav4_bshd_forward_varlen; no reference counterpart) ----
     def varlen_args(self, q, k, v, o, lse, cu_q, cu_k, max_q, max_k, scale=None) -> VarlenArgs:

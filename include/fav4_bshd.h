@@ -102,3 +102,25 @@ struct Fav4VarlenArgs {
 // max_seqlen * heads * 256 >= 2^32), else the launch status.  Allocates
 // nothing and never synchronizes.
 extern "C" int fav4_bshd_forward_varlen(const Fav4VarlenArgs* args, int causal, hipStream_t stream);
+
+// ---- Arbitrary strides -----------------------------------------------------
+// No counterpart in the reference.  Q / O are read as [B, Sq, H, 128] and K /
+// V as [B, Sk, kv_heads, 128] views with the element (BF16) strides given per
+// tensor; the 128 head dims must be contiguous.  Covers BHSD
+// ([B, H, S, 128]: batch = H*S*128, seq = 128, head = S*128), packed QKV
+// ([B, S, 3, H, 128]: seq = 3*H*128) and other views.  LSE stays [B, H, Sq].
+// Query head h reads K/V head h / (heads / kv_heads).  O rows must not
+// overlap each other or Q/K/V (results are undefined otherwise).
+struct Fav4Strides {
+    long long batch, seq, head;
+};
+// Returns 0, hipErrorInvalidValue (1) before any HIP call for the checks of
+// fav4_bshd_forward (except the contiguous-BSHD overflow limits) plus: NULL
+// strides, a negative batch / head stride, a seq stride <= 0, a stride that
+// is not a multiple of 8 elements, kv_heads not dividing heads, one
+// (batch, head) slice spanning 4 GiB or more, or a view spanning more than
+// 2^48 bytes; else the launch status.  Same
+// configs and numerics as fav4_bshd_forward (bitwise equal on the same data).
+extern "C" int fav4_bshd_forward_strided(const Fav4Args* args, int kv_heads, const Fav4Strides* q,
+                                         const Fav4Strides* k, const Fav4Strides* v, const Fav4Strides* o,
+                                         int causal, int config, hipStream_t stream);

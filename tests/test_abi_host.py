@@ -47,7 +47,7 @@ def test_exports_exactly_the_c_abi():
     public = {n for n in names if not n.startswith("_")}
     assert public == {"fav4_bshd_forward", "fav4_bshd_select_config", "fav4_bshd_forward_splitkv",
                       "fav4_bshd_splitkv_workspace_size", "fav4_bshd_splitkv_select", "fav4_bshd_forward_gqa",
-                      "fav4_bshd_forward_varlen"}, public
+                      "fav4_bshd_forward_varlen", "fav4_bshd_forward_strided"}, public
 
 
 def test_ctypes_layout_matches_reference(Args):
@@ -270,3 +270,64 @@ def test_varlen_rejects_bad_causal(lib, causal):
     a = load_package().VarlenArgs(**_vgood())
     assert lib.fav4_bshd_forward_varlen(C.byref(a), causal, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fav4_bshd_forward_varlen(None, 0, None) == HIP_ERROR_INVALID_VALUE
+
+
+# ---- arbitrary strides -------------------------------------------------------
+def _strided_call(lib, a, kv_heads, strides, causal=0, config=0):
+    S = load_package().Strides
+    st = [C.byref(S(*x)) if x is not None else None for x in strides]
+    return lib.fav4_bshd_forward_strided(C.byref(a) if a is not None else None, kv_heads, *st, causal, config, None)
+
+
+def _bshd_strides(b, s, h):
+    return (s * h * 128, h * 128, 128)
+
+
+def test_strides_struct_layout():
+    S = load_package().Strides
+    assert C.sizeof(S) == 24 and S.batch.offset == 0 and S.seq.offset == 8 and S.head.offset == 16
+
+
+SBAD = [
+    ("q_seq_odd", 0, (4096 * 4 * 128, 4 * 128 + 4, 128)),
+    ("k_head_neg", 1, (4096 * 4 * 128, 4 * 128, -128)),
+    ("v_seq_zero", 2, (4096 * 4 * 128, 0, 128)),
+    ("o_batch_neg", 3, (-8, 4 * 128, 128)),
+    ("q_head_odd", 0, (4096 * 4 * 128, 4 * 128, 129)),
+    ("o_span_2p48", 3, (1 << 47, 4 * 128, 128)),   # 2 batches 2^48 bytes apart
+]
+
+
+@pytest.mark.parametrize("name,which,bad", SBAD, ids=[x[0] for x in SBAD])
+def test_strided_rejects_bad_strides(lib, Args, name, which, bad):
+    a = Args(**_good(Args))
+    strides = [_bshd_strides(2, 256, 4)] * 4
+    strides[which] = bad
+    assert _strided_call(lib, a, 4, strides) == HIP_ERROR_INVALID_VALUE
+
+
+def test_strided_rejects_oversized_slice_and_nulls(lib, Args):
+    a = Args(**_good(Args))                           # sq = sk = 256
+    ok = [_bshd_strides(2, 256, 4)] * 4
+    # 255 rows x 2^24 elements x 2 bytes > 4 GiB for one (batch, head) slice
+    for which in range(4):
+        st = list(ok)
+        st[which] = (0, 1 << 24, 128)
+        assert _strided_call(lib, a, 4, st) == HIP_ERROR_INVALID_VALUE, which
+        st[which] = None
+        assert _strided_call(lib, a, 4, st) == HIP_ERROR_INVALID_VALUE, which
+    assert _strided_call(lib, None, 4, ok) == HIP_ERROR_INVALID_VALUE
+    for kvh in (0, 3, 8, -1):
+        assert _strided_call(lib, a, kvh, ok) == HIP_ERROR_INVALID_VALUE, kvh
+    assert _strided_call(lib, a, 4, ok, causal=2) == HIP_ERROR_INVALID_VALUE
+    assert _strided_call(lib, a, 4, ok, config=4) == HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.parametrize("name,change", BAD[:14] + BAD[18:], ids=[x[0] for x in BAD[:14] + BAD[18:]])
+def test_strided_applies_forward_checks(lib, Args, name, change):
+    """The pointer / dimension / scale / alignment checks of fav4_bshd_forward apply too."""
+    f = _good(Args)
+    f.update(change)
+    a = Args(**f)
+    st = [_bshd_strides(2, 256, 4)] * 4
+    assert _strided_call(lib, a, max(1, min(4, a.heads if a.heads > 0 else 1)), st) == HIP_ERROR_INVALID_VALUE
