@@ -7,6 +7,7 @@
 #include "bshd_kernel.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstdint>
@@ -94,11 +95,16 @@ struct SplitPlan {
     int splits, tps;   // chunks and key tiles per chunk
 };
 
+// CU count of the current device (256 if it cannot be read), cached per
+// device after the first query.
 int device_cus() {
+    static std::atomic<int> cache[64];
     int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    const bool slot = dev >= 0 && dev < 64;
+    if (slot && (cus = cache[dev].load(std::memory_order_relaxed)) > 0) return cus;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (slot) cache[dev].store(cus, std::memory_order_relaxed);
     return cus;
 }
 

@@ -55,6 +55,32 @@ def test_headline_b32h8s4096_all_configs(gpu_runner, causal):
         _check_sampled(gpu_runner, torch, q, k, v, causal, config, with_lse=(config == 0), pairs=PAIRS)
 
 
+@pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
+@pytest.mark.parametrize("shape", [(8, 16, 2048, 2048), (8, 16, 1030, 1950)], ids=["even_tiles", "odd_tiles"])
+def test_slices_match_isolated_launches(gpu_runner, shape, causal):
+    """The result of a (b, h) slice must not depend on the rest of the launch
+    (grid size, item order, XCD mapping, even or odd key-tile counts): every
+    slice of a 128-head launch is bitwise equal to the same slice launched
+    alone."""
+    import torch
+    b, h, sq, sk = shape
+    q, k, v = _gpu_inputs(torch, b, h, sq, sk, seed=77)
+    for config in (1, 2):
+        print(f"  slices {shape} causal={causal} config={config}", flush=True)
+        o = torch.full_like(q, float("nan"))
+        lse = torch.full((b, h, sq), float("nan"), device="cuda", dtype=torch.float32)
+        gpu_runner.call(q, k, v, o, lse, causal, config)
+        for bb in range(b):
+            for hh in range(h):
+                qs, ks, vs = (x[bb:bb + 1, :, hh:hh + 1].contiguous() for x in (q, k, v))
+                os_ = torch.full_like(qs, float("nan"))
+                ls = torch.full((1, 1, sq), float("nan"), device="cuda", dtype=torch.float32)
+                gpu_runner.call(qs, ks, vs, os_, ls, causal, config)
+                assert torch.equal(o[bb, :, hh].view(torch.int16), os_[0, :, 0].view(torch.int16)), (bb, hh)
+                assert torch.equal(lse[bb, hh].view(torch.int32), ls[0, 0].view(torch.int32)), (bb, hh)
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("s", [512, 1024, 8192, 16384, 32768])
 def test_long_sequence_sweep(gpu_runner, s):
     """B32 H8 D128, S in {512, 1024, 8192, 16384, 32768}, dense and top-left causal."""
