@@ -109,7 +109,9 @@ int device_cus() {
 }
 
 // Chunking of the key range a row can see (top-left causal never shows a key
-// past sq - 1); `req` = 0 picks enough chunks for about two workgroups per CU.
+// past sq - 1); `req` = 0 picks enough chunks for one workgroup per CU (an
+// 8-wave workgroup fills a CU's register file; more chunks only add merge
+// traffic and per-chunk pipeline fill).
 // The count is then rounded so that no chunk starts past that range.
 SplitPlan split_plan(const Fav4Args& a, int causal, int req) {
     const int tiles = (a.sq + SPLIT_BM - 1) / SPLIT_BM;
@@ -118,7 +120,7 @@ SplitPlan split_plan(const Fav4Args& a, int causal, int req) {
     int64_t splits = req;
     if (splits == 0) {
         const int64_t items = int64_t(a.batch) * a.heads * tiles;
-        splits = (2 * int64_t(device_cus()) + items - 1) / items;
+        splits = (int64_t(device_cus()) + items - 1) / items;
         splits = std::min<int64_t>(splits, std::min(AUTO_MAX_SPLITS, std::max(1, ktiles / MIN_TILES_PER_SPLIT)));
     }
     splits = std::max<int64_t>(1, std::min<int64_t>(splits, ktiles));

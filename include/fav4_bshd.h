@@ -48,7 +48,7 @@ extern "C" int fav4_bshd_select_config(const Fav4Args* args);
 // log-sum-exp.  Results match fav4_bshd_forward within the same tolerances
 // (not bitwise: the chunks' BF16 weights are rounded against their own base).
 // Same argument contract as fav4_bshd_forward (config is always Auto), plus:
-//  * splits: 0 = library choice (about two workgroups per CU, >= 256 keys per
+//  * splits: 0 = library choice (about one workgroup per CU, >= 256 keys per
 //    chunk, at most 64 chunks), else 1..256 (clamped to the key tiles);
 //    splits resolving to 1 run fav4_bshd_forward and need no workspace;
 //  * workspace: caller-owned device memory, 256-byte aligned, at least

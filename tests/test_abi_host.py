@@ -138,12 +138,12 @@ def test_runner_rejects_host_tensors():
 def _split_plan(b, h, sq, sk, splits, cus=None, causal=False):
     """Closed form of the split plan: 64-key tiles over the keys a row can see
     (min(sk, sq) for top-left causal), 256-row q tiles; splits=0 picks
-    ceil(2*CUs / items) capped by min(64, ktiles // 4); then tiles-per-chunk and the
+    ceil(CUs / items) capped by min(64, ktiles // 4); then tiles-per-chunk and the
     final count so that no chunk is empty."""
     ktiles = -(-(min(sk, sq) if causal else sk) // 64)
     if splits == 0:
         items = b * h * -(-sq // 256)
-        splits = min(-(-2 * cus // items), min(64, max(1, ktiles // 4)))
+        splits = min(-(-cus // items), min(64, max(1, ktiles // 4)))
     splits = max(1, min(splits, ktiles))
     tps = -(-ktiles // splits)
     return -(-ktiles // tps), tps
@@ -175,9 +175,11 @@ def test_splitkv_auto_plan(lib, Args, shape):
 
 
 def test_splitkv_plan_examples():
-    # B1 H8 Sq1024 Sk32768 (32 items, 512 key tiles): 16 chunks of 32 tiles;
+    # B1 H8 Sq1024 Sk32768 (32 items, 512 key tiles): 8 chunks of 64 tiles;
     # the headline B32 H8 S4096 needs no split; 79 key tiles in 5 chunks of 16.
-    assert _split_plan(1, 8, 1024, 32768, 0, cus=256) == (16, 32)
+    assert _split_plan(1, 8, 1024, 32768, 0, cus=256) == (8, 64)
+    # decode, B32 H8 Sq1 Sk8192: 256 items already fill the CUs
+    assert _split_plan(32, 8, 1, 8192, 0, cus=256)[0] == 1
     assert _split_plan(32, 8, 4096, 4096, 0, cus=256)[0] == 1
     assert _split_plan(2, 3, 300, 5000, 5) == (5, 16)
     assert _split_plan(1, 1, 256, 65536, 0, cus=256) == (64, 16)

@@ -90,7 +90,7 @@ def test_splitkv_single_chunk_is_the_plain_forward(gpu_runner):
 
 @pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
 def test_splitkv_long_keys_sampled_rows(gpu_runner, causal):
-    """The shape split-KV is for: B1 H8 Sq1024 Sk32768 (32 q tiles; Auto -> 16 chunks
+    """The shape split-KV is for: B1 H8 Sq1024 Sk32768 (32 q tiles; Auto -> 8 chunks
     dense, 4 causal, where rows see only the first 1024 keys), checked on the
     reference's sampled rows for every head."""
     import torch
@@ -100,7 +100,7 @@ def test_splitkv_long_keys_sampled_rows(gpu_runner, causal):
     q, k, v = mk(1024), mk(32768), mk(32768)
     o = torch.full_like(q, float("nan"))
     lse = torch.full((1, 8, 1024), float("nan"), device="cuda", dtype=torch.float32)
-    assert gpu_runner.splitkv_select(1, 8, 1024, 32768, causal) == (4 if causal else 16)
+    assert gpu_runner.splitkv_select(1, 8, 1024, 32768, causal) == (4 if causal else 8)
     print(f"  splitkv B1 H8 1024x32768 causal={causal} auto", flush=True)
     gpu_runner.call_splitkv(q, k, v, o, lse, causal, 0)
     torch.cuda.synchronize()
