@@ -504,13 +504,24 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
                 }
             }
         } else if constexpr (STAGES == 2) {
-            for (; t + 1 < nfull; t += 2) {
-                step(S0{}, Plain{}, t);
-                step(S1{}, Plain{}, t + 1);
-            }
-            for (; t < ntiles; ++t) {
-                if (t & 1) step(S1{}, Masked{}, t);
-                else step(S0{}, Masked{}, t);
+            if (qw >= a.sq) {
+                // All 32 rows of this wave lie past sq (tail q tile): it only
+                // keeps the loop's DMA and barrier sequence.  Deciding once per
+                // q tile keeps the branch out of the step body.
+                for (; t < ntiles; ++t) {
+                    wait_vmem();
+                    __syncthreads();
+                    issue(t + 1);
+                }
+            } else {
+                for (; t + 1 < nfull; t += 2) {
+                    step(S0{}, Plain{}, t);
+                    step(S1{}, Plain{}, t + 1);
+                }
+                for (; t < ntiles; ++t) {
+                    if (t & 1) step(S1{}, Masked{}, t);
+                    else step(S0{}, Masked{}, t);
+                }
             }
         } else {
             for (; t + 2 < nfull; t += 3) {
@@ -690,13 +701,23 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
             using Masked = std::integral_constant<bool, true>;
             int t = t0;
             const int tp = min(t1, nfull);
-            for (; t + 1 < tp; t += 2) {
-                step(S0{}, Plain{}, t);
-                step(S1{}, Plain{}, t + 1);
-            }
-            for (; t < t1; ++t) {
-                if ((t - t0) & 1) step(S1{}, Masked{}, t);
-                else step(S0{}, Masked{}, t);
+            if (qw >= a.sq) {
+                // Rows all past sq (decode: 7 of 8 waves): only the DMA and
+                // barrier sequence of the loop below.
+                for (; t < t1; ++t) {
+                    wait_vmem();
+                    __syncthreads();
+                    if (t + 1 < t1) issue(t + 1);
+                }
+            } else {
+                for (; t + 1 < tp; t += 2) {
+                    step(S0{}, Plain{}, t);
+                    step(S1{}, Plain{}, t + 1);
+                }
+                for (; t < t1; ++t) {
+                    if ((t - t0) & 1) step(S1{}, Masked{}, t);
+                    else step(S0{}, Masked{}, t);
+                }
             }
         }
 
@@ -859,13 +880,23 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
             using Plain = std::integral_constant<bool, false>;
             using Masked = std::integral_constant<bool, true>;
             int t = 0;
-            for (; t + 1 < nfull; t += 2) {
-                step(S0{}, Plain{}, t);
-                step(S1{}, Plain{}, t + 1);
-            }
-            for (; t < ntiles; ++t) {
-                if (t & 1) step(S1{}, Masked{}, t);
-                else step(S0{}, Masked{}, t);
+            if (qw >= sq) {
+                // Rows all past this sequence's end: only the DMA and barrier
+                // sequence of the loop below.
+                for (; t < ntiles; ++t) {
+                    wait_vmem();
+                    __syncthreads();
+                    if (t + 1 < ntiles) issue(t + 1);
+                }
+            } else {
+                for (; t + 1 < nfull; t += 2) {
+                    step(S0{}, Plain{}, t);
+                    step(S1{}, Plain{}, t + 1);
+                }
+                for (; t < ntiles; ++t) {
+                    if (t & 1) step(S1{}, Masked{}, t);
+                    else step(S0{}, Masked{}, t);
+                }
             }
         }
 
