@@ -114,3 +114,24 @@ def test_splitkv_long_keys_sampled_rows(gpu_runner, causal):
     sel = lambda x: np.stack([x[0, :, hh] for _, hh in heads])
     e = orc.errors(sel(got), got_lse[0], sel(ref), ref_lse[0])
     assert orc.check_north_star_tolerance(e) and orc.check_reference_tolerance(e), e
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
+def test_splitkv_decode_at_scale(gpu_runner, causal):
+    """Decode: B4 H8, one query against 65536 keys (Auto chunks; 7 of 8 waves only
+    stream K/V), every row and head against the FP64 oracle."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    mk = lambda s: torch.randn((4, s, 8, 128), device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
+    q, k, v = mk(1), mk(65536), mk(65536)
+    o = torch.full_like(q, float("nan"))
+    lse = torch.full((4, 8, 1), float("nan"), device="cuda", dtype=torch.float32)
+    splits = gpu_runner.splitkv_select(4, 8, 1, 65536, causal)
+    print(f"  splitkv decode B4 H8 1x65536 causal={causal} splits={splits}", flush=True)
+    assert splits == (1 if causal else 8)
+    gpu_runner.call_splitkv(q, k, v, o, lse, causal, 0)
+    torch.cuda.synchronize()
+    ref, ref_lse = orc.attention_fp64(to_host_bits(q), to_host_bits(k), to_host_bits(v), orc.DEFAULT_SCALE, causal)
+    e = orc.errors(to_host_bits(o), lse.cpu().numpy(), ref, ref_lse)
+    assert orc.check_north_star_tolerance(e) and orc.check_reference_tolerance(e), e
