@@ -144,30 +144,67 @@ def time_graph(torch, fn, steps, warmup, observations, stream):
     return samples
 
 
+def cpu_info():
+    """(model name, socket count) of the host CPU from /proc/cpuinfo."""
+    model, sockets = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("physical id"):
+                    sockets.add(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return model, max(1, len(sockets))
+
+
+def _attention_fp32_slice(qb, kb, vb, bh, scale):
+    """Dense FP32 attention of one (b, h) slice (numpy, textbook form)."""
+    from oracle import attention as orc
+    b, h = bh
+    q = orc.bf16_to_f32(qb[b, :, h]).reshape(qb.shape[1], -1)
+    k = orc.bf16_to_f32(kb[b, :, h]).reshape(kb.shape[1], -1)
+    v = orc.bf16_to_f32(vb[b, :, h]).reshape(vb.shape[1], -1)
+    s = (q @ k.T) * np.float32(scale)
+    s -= s.max(axis=1, keepdims=True)
+    p = np.exp(s)
+    return (p @ v) / p.sum(axis=1, keepdims=True)
+
+
 def cpu_baseline(torch, orc, q, k, v, budget_s):
-    """FP64 oracle on host cores over (b, h) slices of the dense workload until
-    the time budget is spent.  Threads: one slice per worker, BLAS single-threaded."""
+    """FP64 oracle (and an FP32 textbook attention) on host cores over (b, h)
+    slices of the dense workload until each time budget is spent.  Threads: one
+    slice per worker, BLAS single-threaded."""
     from concurrent.futures import ThreadPoolExecutor
     from threadpoolctl import threadpool_limits
     b, s, h, d = q.shape
     cores = min(len(os.sched_getaffinity(0)), 16)
     qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
     pairs = [(i, j) for i in range(b) for j in range(h)]
-    done = 0
-    t0 = time.perf_counter()
-    with threadpool_limits(1), ThreadPoolExecutor(cores) as ex:
-        while done < len(pairs) and time.perf_counter() - t0 < budget_s:
-            chunk = pairs[done:done + cores]
-            list(ex.map(lambda p: orc.attention_fp64(qb, kb, vb, orc.DEFAULT_SCALE, False, heads=[p]),
-                        chunk))
-            done += len(chunk)
-    elapsed = time.perf_counter() - t0
-    flop = orc.flops(1, 1, s, s, False) * done
-    return dict(value=flop / elapsed / 1e12, unit="TFLOP/s", cores=cores, kind="port",
+
+    def run(fn, budget):
+        done = 0
+        t0 = time.perf_counter()
+        with threadpool_limits(1), ThreadPoolExecutor(cores) as ex:
+            while done < len(pairs) and time.perf_counter() - t0 < budget:
+                chunk = pairs[done:done + cores]
+                list(ex.map(fn, chunk))
+                done += len(chunk)
+        return done, time.perf_counter() - t0
+
+    done, elapsed = run(lambda p: orc.attention_fp64(qb, kb, vb, orc.DEFAULT_SCALE, False, heads=[p]), budget_s)
+    done32, elapsed32 = run(lambda p: _attention_fp32_slice(qb, kb, vb, p, orc.DEFAULT_SCALE), budget_s / 2)
+    flop1 = orc.flops(1, 1, s, s, False)
+    model, sockets = cpu_info()
+    return dict(value=flop1 * done / elapsed / 1e12, unit="TFLOP/s", cores=cores, kind="port",
                 sample=f"FP64 numpy oracle, {done} of {len(pairs)} (b,h) slices of B{b} H{h} "
                        f"S{s} D{d} dense, {elapsed:.1f} s on {cores} threads (one slice per thread, "
                        f"single-threaded BLAS); extrapolated whole-job time "
-                       f"{elapsed * len(pairs) / done:.1f} s")
+                       f"{elapsed * len(pairs) / done:.1f} s",
+                fp32=dict(value=round(flop1 * done32 / elapsed32 / 1e12, 4), unit="TFLOP/s",
+                          sample=f"FP32 numpy textbook attention, {done32} slices in {elapsed32:.1f} s"),
+                cpu_model=model, sockets=sockets)
 
 
 def time_eager(torch, fn, steps, warmup, stream):
@@ -500,6 +537,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(dense["us"] / 1000.0, 5),
+        "median_us_per_step": round(dense["median_us"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -515,6 +553,7 @@ def main():
     if True in results:
         c = results[True]
         line["causal"] = dict(value=round(c["tflops"], 2), unit="TFLOP/s", us_per_launch=round(c["us"], 3),
+                              median_us_per_launch=round(c["median_us"], 3),
                               frac_of_peak=round(c["tflops"] / PEAK_BF16_TFLOPS, 4),
                               samples_us=[round(x, 2) for x in c["samples_us"]])
     line["dense_samples_us"] = [round(x, 2) for x in dense["samples_us"]]
