@@ -19,8 +19,9 @@
 //    (no LDS round trip); the V operand comes from ds_read_b64_tr_b16.
 //  * Key tiles that no row of the workgroup masks run a branch-free body;
 //    only the causal-diagonal and key-tail tiles run the masked body, where
-//    32-key blocks entirely hidden from a wave are skipped and the rest get
-//    the element mask.  Key tiles entirely above the diagonal are never loaded.
+//    QK^T skips 32-key blocks entirely hidden from a wave, the rest get the
+//    element mask, and a wave skips a causal tile entirely above its rows.
+//    Key tiles entirely above the diagonal are never loaded.
 //  * O is normalised by the sum of the BF16-rounded weights that entered the
 //    PV product (see the epilogue); the LSE uses the FP32 sum as the reference.
 #pragma once
@@ -230,23 +231,22 @@ __device__ __forceinline__ void attend_tail(f32x16 (&s)[BN / 32], const unsigned
     bf16x8 p[U];
     exp_unit<LSE>(s[0], 0, p[0], c, scale2);
     apply_rescale(st, c);
+    // PV runs for every unit, masked tiles included: the weights of a hidden
+    // block are exactly 0, and a branch here would split the exp/PV overlap
+    // (measured: +1.5% causal over skipping hidden blocks).
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int kb = u >> 1;
-        const bool act = block_active<MASKED, CAUSAL>(start + kb * 32, sk, qw);
         if (u + 1 < U) exp_unit<LSE>(s[(u + 1) >> 1], (u + 1) & 1, p[u + 1], c, scale2);
-        if (!MASKED || act) {
-            const unsigned char* vb = vs + u * 16 * ROW_BYTES;
-            bf16x8 vop[4];
+        const unsigned char* vb = vs + u * 16 * ROW_BYTES;
+        bf16x8 vop[4];
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const bf16x4 lo = lds_read_tr(vb + off.v[0][db]);
-                const bf16x4 hi = lds_read_tr(vb + off.v[1][db]);
-                vop[db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            }
-#pragma unroll
-            for (int db = 0; db < 4; ++db) st.o[db] = mfma32(vop[db], p[u], st.o[db]);
+        for (int db = 0; db < 4; ++db) {
+            const bf16x4 lo = lds_read_tr(vb + off.v[0][db]);
+            const bf16x4 hi = lds_read_tr(vb + off.v[1][db]);
+            vop[db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
+#pragma unroll
+        for (int db = 0; db < 4; ++db) st.o[db] = mfma32(vop[db], p[u], st.o[db]);
     }
     st.lb = st.lb * c.alpha + xhalf_sum(c.pb0 + c.pb1);
     if constexpr (LSE) st.l = st.l * c.alpha + xhalf_sum((c.part[0] + c.part[1]) + (c.part[2] + c.part[3]));
@@ -422,8 +422,11 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
             wait_vmem_keep<2 * DMA * (AHEAD - 1)>();
             __syncthreads();
             issue(t + AHEAD);
-            attend_fused<BN, MASKED, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st, t == 0, t * BN, a.sk, qw,
-                                                  row, half, scale2);
+            // A causal tile entirely above this wave's rows changes nothing
+            // (tile 0 never is): the wave only keeps the DMA and barriers.
+            if (!(MASKED && CAUSAL) || t * BN <= qw + 31)
+                attend_fused<BN, MASKED, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st, t == 0, t * BN, a.sk, qw,
+                                                      row, half, scale2);
         };
         using S0 = std::integral_constant<int, 0>;
         using S1 = std::integral_constant<int, 1>;
@@ -884,8 +887,10 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
                 wait_vmem();
                 __syncthreads();
                 if (t + 1 < ntiles) issue(t + 1);
-                attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st, t == 0,
-                                                                       t * BN, sk, qw, row, half, scale2);
+                // A causal tile entirely above this wave's rows changes nothing.
+                if (!(decltype(masked_c)::value && CAUSAL) || t * BN <= qw + 31)
+                    attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st,
+                                                                           t == 0, t * BN, sk, qw, row, half, scale2);
             };
             using S0 = std::integral_constant<int, 0>;
             using S1 = std::integral_constant<int, 1>;
