@@ -295,7 +295,7 @@ def splitkv_report(torch, orc, runner, args, stream, b=1, h=8, sq=1024, sk=32768
                 fn()
             torch.cuda.synchronize()
             err, _ = check_rows(torch, orc, q, k, v, o, causal, [(0, 0), (0, h - 1)])
-            if not orc.check_north_star_tolerance(err):
+            if not orc.check_acceptance_tolerance(err):
                 raise SystemExit(f"split-KV report: {name} check failed (causal={causal}): {err}")
             us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream))
             res[name] = dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1))
@@ -328,7 +328,7 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
         torch.cuda.synchronize()
         for qc, kc, vc, oc, causal in checks():
             err, _ = check_rows(torch, orc, qc, kc, vc, oc, causal, [(0, 0), (0, h - 1)])
-            if not orc.check_north_star_tolerance(err):
+            if not orc.check_acceptance_tolerance(err):
                 raise SystemExit(f"api report: {name} check failed: {err}")
         us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream))
         print(f"# {name}: {us:.1f} us, {flop / us / 1e6:.1f} TFLOP/s", file=sys.stderr, flush=True)
@@ -453,7 +453,7 @@ def main():
     global _TELEMETRY
     _TELEMETRY = not args.no_telemetry
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+        print(json.dumps({"error": "this library runs on one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
@@ -482,7 +482,7 @@ def main():
                 fn()
             torch.cuda.synchronize()
             check, _ = check_rows(torch, orc, q, k, v, o, causal, pairs)
-            if not orc.check_north_star_tolerance(check):
+            if not orc.check_acceptance_tolerance(check):
                 raise SystemExit(f"sampled-row check failed (causal={causal}): {check}")
         samples = time_graph(torch, fn, args.steps, args.warmup, args.observations, stream)
         flop = orc.flops(b, h, s, s, causal)

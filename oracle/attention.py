@@ -1,6 +1,6 @@
 """CPU oracle for the BF16 BSHD D=128 attention forward (TEST INFRASTRUCTURE ONLY).
 
-This module is the checker, never the product: only ``tests/``, the package's
+This module checks results and is never the product: only ``tests/``, the package's
 ``smoke`` check and ``bench.py``'s ``cpu_baseline`` leg may import it.  The
 product path (``libfav4_bshd.so``) never calls into it and has no CPU fallback.
 
@@ -13,7 +13,7 @@ What it restates, and from where (paths relative to the reference repo):
   The reference divides by ``math.sqrt(128)``; the ABI carries the scale as a
   float32, so the oracle multiplies by that float32 value in FP64.  For
   1/sqrt(128) the two differ by < 3e-8 relative.
-* ``errors`` / ``check_reference_tolerance`` / ``check_north_star_tolerance``
+* ``errors`` / ``check_reference_tolerance`` / ``check_acceptance_tolerance``
   -- the error metrics and BF16 tolerances of ``benchmarks/bshd.py:22-32``
   (elementwise |o-ref| <= 0.01 + 0.01|ref|, RMS-relative <= 0.005, LSE
   max-abs <= 2e-4, all finite) and the looser acceptance bar of the port
@@ -261,7 +261,7 @@ def check_reference_tolerance(e: dict) -> bool:
             and (e["lse_max_abs"] is None or e["lse_max_abs"] <= 2e-4))
 
 
-def check_north_star_tolerance(e: dict) -> bool:
+def check_acceptance_tolerance(e: dict) -> bool:
     """The port's acceptance bar: max-abs <= 2e-2, LSE max-abs <= 1e-3, finite."""
     return (e["finite"] and e["max_abs"] <= 2e-2
             and (e["lse_max_abs"] is None or e["lse_max_abs"] <= 1e-3))

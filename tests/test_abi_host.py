@@ -1,7 +1,7 @@
 """Host-only checks of the C ABI (no GPU needed, no compute call is made).
 
 The library must export the two entry points of the reference header
-(include/fav4_bshd.h:19-20) plus this build's split-KV, GQA and varlen ones, lay
+(include/fav4_bshd.h:19-20) plus the split-KV, GQA, varlen and strided additions, lay
 out Fav4Args byte for byte like the reference (include/fav4_bshd.h:4-10), and
 reject bad arguments with hipErrorInvalidValue before touching HIP, as
 src/bshd.hip:27-34 does.  The split-KV size / plan queries are checked
