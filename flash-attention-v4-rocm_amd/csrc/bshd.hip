@@ -85,14 +85,23 @@ bool stride_ok(const Fav4Strides* st, int batch, int heads, int rows) {
 }
 
 // ---- split-KV -------------------------------------------------------------
-constexpr int SPLIT_BM = 256, SPLIT_BN = 64;
-constexpr int MAX_SPLITS = 256;          // accepted explicit split counts
-constexpr int AUTO_MAX_SPLITS = 64;      // Auto never goes beyond this
-constexpr int MIN_TILES_PER_SPLIT = 4;   // Auto keeps >= 256 keys per chunk
+constexpr int MIN_TILES_PER_SPLIT = 4;   // Auto keeps >= 4 key tiles per chunk
 constexpr int MAX_SPLIT_SQ = 1 << 22;    // keeps a chunk's O rows under a 4 GiB buffer bound
+constexpr int DECODE_SQ = 32;            // up to this many queries: the one-wave decode shape
+
+// Tile shape of the partial kernel: 8 waves x 256-row q tiles x 64-key tiles
+// (one workgroup fills a CU), or for decode 1 wave x 32 rows x 32-key tiles
+// (three workgroups per CU, each with 48 KiB of LDS).
+struct SplitShape {
+    int bm, bn, wgs_per_cu, auto_max;
+};
+SplitShape split_shape(const Fav4Args& a) {
+    return a.sq <= DECODE_SQ ? SplitShape{32, 32, 3, 128} : SplitShape{256, 64, 1, 64};
+}
 
 struct SplitPlan {
     int splits, tps;   // chunks and key tiles per chunk
+    SplitShape shape;
 };
 
 // CU count of the current device (256 if it cannot be read), cached per
@@ -109,23 +118,24 @@ int device_cus() {
 }
 
 // Chunking of the key range a row can see (top-left causal never shows a key
-// past sq - 1); `req` = 0 picks enough chunks for one workgroup per CU (an
-// 8-wave workgroup fills a CU's register file; more chunks only add merge
-// traffic and per-chunk pipeline fill).
-// The count is then rounded so that no chunk starts past that range.
+// past sq - 1); `req` = 0 picks enough chunks to fill the CUs once (the
+// shape's resident workgroups per CU; more chunks only add merge traffic and
+// per-chunk pipeline fill).  The count is then rounded so that no chunk
+// starts past that range.
 SplitPlan split_plan(const Fav4Args& a, int causal, int req) {
-    const int tiles = (a.sq + SPLIT_BM - 1) / SPLIT_BM;
+    const SplitShape sh = split_shape(a);
+    const int tiles = (a.sq + sh.bm - 1) / sh.bm;
     const int keys = causal ? std::min(a.sk, a.sq) : a.sk;
-    const int ktiles = (keys + SPLIT_BN - 1) / SPLIT_BN;
+    const int ktiles = (keys + sh.bn - 1) / sh.bn;
     int64_t splits = req;
     if (splits == 0) {
         const int64_t items = int64_t(a.batch) * a.heads * tiles;
-        splits = (int64_t(device_cus()) + items - 1) / items;
-        splits = std::min<int64_t>(splits, std::min(AUTO_MAX_SPLITS, std::max(1, ktiles / MIN_TILES_PER_SPLIT)));
+        splits = (int64_t(device_cus()) * sh.wgs_per_cu + items - 1) / items;
+        splits = std::min<int64_t>(splits, std::min(sh.auto_max, std::max(1, ktiles / MIN_TILES_PER_SPLIT)));
     }
     splits = std::max<int64_t>(1, std::min<int64_t>(splits, ktiles));
     const int tps = int((ktiles + splits - 1) / splits);
-    return {(ktiles + tps - 1) / tps, tps};
+    return {(ktiles + tps - 1) / tps, tps, sh};
 }
 
 int64_t split_workspace(const Fav4Args& a, const SplitPlan& p) {
@@ -137,7 +147,7 @@ int64_t split_workspace(const Fav4Args& a, const SplitPlan& p) {
 int split_shape_ok(const Fav4Args* a, int causal, int splits) {
     if (!a || a->batch <= 0 || a->heads <= 0 || a->sq <= 0 || a->sk <= 0 || (causal != 0 && causal != 1) ||
         a->batch > INT_MAX / a->heads || a->heads > INT_MAX / 128 || a->sq > INT_MAX / (a->heads * 128) ||
-        a->sk > INT_MAX / (a->heads * 128) || splits < 0 || splits > MAX_SPLITS || a->sq > MAX_SPLIT_SQ)
+        a->sk > INT_MAX / (a->heads * 128) || splits < 0 || splits > fav4::MAX_SPLITS || a->sq > MAX_SPLIT_SQ)
         return hipErrorInvalidValue;
     return hipSuccess;
 }
@@ -149,21 +159,32 @@ int split_args_ok(const Fav4Args* a, int causal, int splits) {
 
 template <bool CAUSAL>
 int launch_split(const Fav4Args& a, const SplitPlan& p, void* ws, hipStream_t stream) {
-    const int tiles = (a.sq + SPLIT_BM - 1) / SPLIT_BM;
+    const int tiles = (a.sq + p.shape.bm - 1) / p.shape.bm;
     const int64_t total = int64_t(a.batch) * a.heads * tiles * p.splits;
     const int64_t rows = int64_t(a.batch) * a.heads * a.sq;
-    if (total > INT_MAX || (rows + 7) / 8 > INT_MAX) return hipErrorInvalidValue;
+    if (total > INT_MAX || rows > INT_MAX) return hipErrorInvalidValue;
     fav4::SplitArgs sp;
     sp.o_part = static_cast<float*>(ws);
     sp.lse_part = sp.o_part + int64_t(p.splits) * rows * fav4::D;
     sp.splits = p.splits;
     sp.tps = p.tps;
     const int grid = int(total < MAX_GRID ? total : MAX_GRID);
-    hipLaunchKernelGGL((fav4::fwd_kernel_split<SPLIT_BN, CAUSAL>), dim3(grid), dim3(512), 0, stream, a, sp, a.heads,
-                       tiles, int(total));
+    if (p.shape.bm == 32)
+        hipLaunchKernelGGL((fav4::fwd_kernel_split<32, CAUSAL, 1>), dim3(grid), dim3(64), 0, stream, a, sp, a.heads,
+                           tiles, int(total));
+    else
+        hipLaunchKernelGGL((fav4::fwd_kernel_split<64, CAUSAL, 8>), dim3(grid), dim3(512), 0, stream, a, sp, a.heads,
+                           tiles, int(total));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(fav4::combine_kernel, dim3(unsigned((rows + 7) / 8)), dim3(256), 0, stream, a, sp);
+    // Lane groups per merged row: one per 8 chunks, at most 8 (one workgroup).
+    const int per = p.splits <= 8 ? 1 : p.splits <= 16 ? 2 : p.splits <= 32 ? 4 : 8;
+    const int64_t row_blocks = (rows * per + 7) / 8;
+    const unsigned blocks = unsigned(row_blocks < MAX_GRID ? row_blocks : MAX_GRID);
+    if (per == 1) hipLaunchKernelGGL(fav4::combine_kernel<1>, dim3(blocks), dim3(256), 0, stream, a, sp);
+    else if (per == 2) hipLaunchKernelGGL(fav4::combine_kernel<2>, dim3(blocks), dim3(256), 0, stream, a, sp);
+    else if (per == 4) hipLaunchKernelGGL(fav4::combine_kernel<4>, dim3(blocks), dim3(256), 0, stream, a, sp);
+    else hipLaunchKernelGGL(fav4::combine_kernel<8>, dim3(blocks), dim3(256), 0, stream, a, sp);
     return hipGetLastError();
 }
 

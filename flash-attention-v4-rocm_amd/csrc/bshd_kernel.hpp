@@ -569,10 +569,10 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-KV: the key range of every (batch, head, 256-row q tile) is cut into
-// `splits` chunks of `tps` key tiles, each chunk is attended by its own
-// workgroup (same tile body as fwd_kernel<8, BN, ...>, 3 LDS stages), and a
-// second kernel merges the chunks.  For few (b, h, q tile) items and long
+// Split-KV: the key range of every (batch, head, q tile) is cut into `splits`
+// chunks of `tps` key tiles, each chunk is attended by its own workgroup (same
+// tile body as fwd_kernel, 3 LDS stages), and a second kernel merges the
+// chunks.  For few (b, h, q tile) items and long
 // keys this fills the GPU where one workgroup per item cannot.
 // Workspace (FP32, caller-owned):
 //   o_part  [splits][B*H][sq][128]  O of the chunk, normalised by its own
@@ -594,10 +594,13 @@ struct SplitArgs {
 // distance 2).  Long-key prefill chunks run as fast as with two; decode-like
 // chunks, where one wave computes and the kernel mostly streams K/V, gain up
 // to 10% (measured), since the DMA latency rather than the MFMAs bounds a tile.
-template <int BN, bool CAUSAL>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// WAVES = 8, BN = 64: long-key prefill chunks (256-row q tiles).  WAVES = 1,
+// BN = 32: decode (sq <= 32): one wave per workgroup and 48 KiB of LDS, so
+// three workgroups share a CU and every resident wave computes.
+template <int BN, bool CAUSAL, int WAVES = 8>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int total) {
-    constexpr int WAVES = 8, BM = 256, STAGES = 3;
+    constexpr int BM = WAVES * 32, STAGES = 3;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
     constexpr int STAGE_BYTES = 2 * TILE_BYTES;
     constexpr int DMA = BN / 4 / WAVES;
@@ -939,41 +942,121 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
     }
 }
 
-// Merge of the split-KV chunks: one 32-lane group per (b, h, row), 4 output
-// dims per lane; O in BF16 BSHD and the optional FP32 LSE.
+// Merge of the split-KV chunks.  PER groups of 32 lanes share one (b, h, row),
+// so a workgroup of 256 lanes merges 8 / PER rows.  The row's PER * 32 lanes
+// first read the chunks' log-sums side by side (maxima, then weights into LDS
+// and the two sums); group p then accumulates the O of chunks p, p + PER, ...
+// (4 dims per lane) with no branch between the loads, and the groups' partial
+// sums are added in LDS.  Many chunks over few rows (decode) thus take a few
+// memory round trips instead of one pair of dependent loads per chunk.
+constexpr int MAX_SPLITS = 256;
+
+__device__ __forceinline__ float max32(float x) {
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 32));
+    return x;
+}
+
+__device__ __forceinline__ float sum32(float x) {
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) x += __shfl_xor(x, m, 32);
+    return x;
+}
+
+template <int PER>
 __global__ __launch_bounds__(256) void combine_kernel(Fav4Args a, SplitArgs sp) {
+    constexpr int RPB = 8 / PER, NT = PER * 32, MAXV = (MAX_SPLITS + NT - 1) / NT;
+    __shared__ float wsh[RPB][MAX_SPLITS];   // chunk weights 2^(lse_b,s - max)
+    __shared__ float2 red_m[8], red_s[8];    // per-group maxima, then sums
+    __shared__ f32x4 part_acc[8][32];
+    const int grp = threadIdx.x >> 5, q4 = threadIdx.x & 31;
+    const int slot = grp / PER, part = grp - slot * PER;
+    const int team = part * 32 + q4;
     const int64_t rows = int64_t(a.batch) * a.heads * a.sq;
-    const int64_t r = int64_t(blockIdx.x) * 8 + (threadIdx.x >> 5);
-    const int q4 = threadIdx.x & 31;
-    if (r >= rows) return;
-    const int64_t bh = r / a.sq;
-    const int row = int(r - bh * a.sq);
     const int64_t slab = rows;                      // rows per chunk
-    float mb = -__builtin_inff(), ml = -__builtin_inff();
-    for (int s = 0; s < sp.splits; ++s) {
-        const float* lp = sp.lse_part + (s * slab + r) * 2;
-        mb = fmaxf(mb, lp[0]);
-        ml = fmaxf(ml, lp[1]);
-    }
-    float den = 0.f, suml = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < sp.splits; ++s) {
-        const float* lp = sp.lse_part + (s * slab + r) * 2;
-        const float w = exp2_native(lp[0] - mb);
-        suml += exp2_native(lp[1] - ml);
-        if (w > 0.f) {
-            const f32x4 x = *reinterpret_cast<const f32x4*>(sp.o_part + (s * slab + r) * D + q4 * 4);
-            acc += w * x;
-            den += w;
+    const int64_t blocks = (rows + RPB - 1) / RPB;
+
+    // Workgroup-uniform loop: every wave reaches every barrier.
+    for (int64_t blk = blockIdx.x; blk < blocks; blk += gridDim.x) {
+        const int64_t r = blk * RPB + slot;
+        const bool live = r < rows;
+        float vb[MAXV], vl[MAXV];
+        float mb = -__builtin_inff(), ml = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < MAXV; ++i) {
+            const int s = team + i * NT;
+            vb[i] = vl[i] = -__builtin_inff();
+            if (live && s < sp.splits) {
+                const float2 v = *reinterpret_cast<const float2*>(sp.lse_part + (s * slab + r) * 2);
+                vb[i] = v.x;
+                vl[i] = v.y;
+            }
+            mb = fmaxf(mb, vb[i]);
+            ml = fmaxf(ml, vl[i]);
         }
+        mb = max32(mb);
+        ml = max32(ml);
+        if (q4 == 0) red_m[grp] = float2{mb, ml};
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            mb = fmaxf(mb, red_m[slot * PER + p].x);
+            ml = fmaxf(ml, red_m[slot * PER + p].y);
+        }
+        float den = 0.f, suml = 0.f;
+#pragma unroll
+        for (int i = 0; i < MAXV; ++i) {
+            const int s = team + i * NT;
+            if (s < sp.splits) {
+                const float w = live ? exp2_native(vb[i] - mb) : 0.f;
+                wsh[slot][s] = w;
+                den += w;
+                if (live) suml += exp2_native(vl[i] - ml);
+            }
+        }
+        den = sum32(den);
+        suml = sum32(suml);
+        if (q4 == 0) red_s[grp] = float2{den, suml};
+        __syncthreads();
+        den = suml = 0.f;
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            den += red_s[slot * PER + p].x;
+            suml += red_s[slot * PER + p].y;
+        }
+
+        // Chunks without a visible key carry weight 0 and O = 0; the test on
+        // the weight keeps them out of the sum exactly.
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        if (live) {
+            const float* op = sp.o_part + r * D + q4 * 4;
+#pragma unroll 4
+            for (int s = part; s < sp.splits; s += PER) {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(op + s * slab * D);
+                const float w = wsh[slot][s];
+                if (w > 0.f) acc += w * x;
+            }
+        }
+        if constexpr (PER > 1) {
+            part_acc[grp][q4] = acc;
+            __syncthreads();
+#pragma unroll
+            for (int p = 1; p < PER; ++p) acc += part_acc[slot * PER + p][q4];
+        }
+        if (live && part == 0) {
+            const f32x4 y = acc * (1.f / den);
+            const int64_t bh = r / a.sq;
+            const int row = int(r - bh * a.sq);
+            const int batch = int(bh / a.heads), head = int(bh - int64_t(batch) * a.heads);
+            const int64_t orow = (int64_t(batch) * a.sq + row) * a.heads + head;
+            const f32x2 y0 = {y[0], y[1]}, y1 = {y[2], y[3]};
+            const bf16x2 b0 = __builtin_convertvector(y0, bf16x2), b1 = __builtin_convertvector(y1, bf16x2);
+            *reinterpret_cast<bf16x4*>(static_cast<char*>(a.o) + orow * ROW_BYTES + q4 * 8) =
+                bf16x4{b0[0], b0[1], b1[0], b1[1]};
+            if (a.lse && q4 == 0) a.lse[r] = (ml + __builtin_amdgcn_logf(suml)) * LN2;
+        }
+        __syncthreads();   // LDS of this row block is reused by the next
     }
-    const f32x4 y = acc * (1.f / den);
-    const int batch = int(bh / a.heads), head = int(bh - int64_t(batch) * a.heads);
-    const int64_t orow = (int64_t(batch) * a.sq + row) * a.heads + head;
-    const f32x2 y0 = {y[0], y[1]}, y1 = {y[2], y[3]};
-    const bf16x2 b0 = __builtin_convertvector(y0, bf16x2), b1 = __builtin_convertvector(y1, bf16x2);
-    *reinterpret_cast<bf16x4*>(static_cast<char*>(a.o) + orow * ROW_BYTES + q4 * 8) = bf16x4{b0[0], b0[1], b1[0], b1[1]};
-    if (a.lse && q4 == 0) a.lse[r] = (ml + __builtin_amdgcn_logf(suml)) * LN2;
 }
 
 }  // namespace fav4

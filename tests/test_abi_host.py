@@ -136,14 +136,17 @@ def test_runner_rejects_host_tensors():
 # ---- split-KV queries -------------------------------------------------------
 
 def _split_plan(b, h, sq, sk, splits, cus=None, causal=False):
-    """Closed form of the split plan: 64-key tiles over the keys a row can see
-    (min(sk, sq) for top-left causal), 256-row q tiles; splits=0 picks
-    ceil(CUs / items) capped by min(64, ktiles // 4); then tiles-per-chunk and the
-    final count so that no chunk is empty."""
-    ktiles = -(-(min(sk, sq) if causal else sk) // 64)
+    """Closed form of the split plan: key tiles over the keys a row can see
+    (min(sk, sq) for top-left causal); 256-row q tiles and 64-key tiles, one
+    workgroup per CU and at most 64 Auto chunks -- or, for sq <= 32 (decode),
+    32-row q tiles, 32-key tiles, three workgroups per CU and at most 128;
+    splits=0 picks ceil(CUs * per_cu / items) capped by min(max, ktiles // 4);
+    then tiles-per-chunk and the final count so that no chunk is empty."""
+    bm, bn, per_cu, amax = (32, 32, 3, 128) if sq <= 32 else (256, 64, 1, 64)
+    ktiles = -(-(min(sk, sq) if causal else sk) // bn)
     if splits == 0:
-        items = b * h * -(-sq // 256)
-        splits = min(-(-cus // items), min(64, max(1, ktiles // 4)))
+        items = b * h * -(-sq // bm)
+        splits = min(-(-(cus * per_cu) // items), min(amax, max(1, ktiles // 4)))
     splits = max(1, min(splits, ktiles))
     tps = -(-ktiles // splits)
     return -(-ktiles // tps), tps
@@ -178,8 +181,11 @@ def test_splitkv_plan_examples():
     # B1 H8 Sq1024 Sk32768 (32 items, 512 key tiles): 8 chunks of 64 tiles;
     # the headline B32 H8 S4096 needs no split; 79 key tiles in 5 chunks of 16.
     assert _split_plan(1, 8, 1024, 32768, 0, cus=256) == (8, 64)
-    # decode, B32 H8 Sq1 Sk8192: 256 items already fill the CUs
-    assert _split_plan(32, 8, 1, 8192, 0, cus=256)[0] == 1
+    # decode, B32 H8 Sq1 Sk8192 (one-wave shape, 256 items, 256 32-key tiles):
+    # 3 chunks of 86 tiles fill three workgroups per CU
+    assert _split_plan(32, 8, 1, 8192, 0, cus=256) == (3, 86)
+    # decode, B1 H8 Sq1 Sk65536: 2048 key tiles, 96 chunks wanted -> 94 of 22
+    assert _split_plan(1, 8, 1, 65536, 0, cus=256) == (94, 22)
     assert _split_plan(32, 8, 4096, 4096, 0, cus=256)[0] == 1
     assert _split_plan(2, 3, 300, 5000, 5) == (5, 16)
     assert _split_plan(1, 1, 256, 65536, 0, cus=256) == (64, 16)

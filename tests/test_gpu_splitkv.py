@@ -118,8 +118,9 @@ def test_splitkv_long_keys_sampled_rows(gpu_runner, causal):
 
 @pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
 def test_splitkv_decode_at_scale(gpu_runner, causal):
-    """Decode: B4 H8, one query against 65536 keys (Auto chunks; 7 of 8 waves only
-    stream K/V), every row and head against the FP64 oracle."""
+    """Decode: B4 H8, one query against 65536 keys (Auto: the one-wave decode
+    shape, 24 chunks of 86 32-key tiles), every row and head against the FP64
+    oracle."""
     import torch
     g = torch.Generator(device="cuda")
     g.manual_seed(5)
@@ -129,9 +130,30 @@ def test_splitkv_decode_at_scale(gpu_runner, causal):
     lse = torch.full((4, 8, 1), float("nan"), device="cuda", dtype=torch.float32)
     splits = gpu_runner.splitkv_select(4, 8, 1, 65536, causal)
     print(f"  splitkv decode B4 H8 1x65536 causal={causal} splits={splits}", flush=True)
-    assert splits == (1 if causal else 8)
+    assert splits == (1 if causal else 24)
     gpu_runner.call_splitkv(q, k, v, o, lse, causal, 0)
     torch.cuda.synchronize()
     ref, ref_lse = orc.attention_fp64(to_host_bits(q), to_host_bits(k), to_host_bits(v), orc.DEFAULT_SCALE, causal)
     e = orc.errors(to_host_bits(o), lse.cpu().numpy(), ref, ref_lse)
     assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), e
+
+
+MANY = [((1, 2, 1, 20000), False), ((2, 3, 17, 9000), False), ((1, 2, 40, 20000), False),
+        ((1, 2, 2048, 2048), True)]
+
+
+@pytest.mark.parametrize("case", MANY, ids=lambda c: "b%dh%d_%dx%d" % c[0] + ("_causal" if c[1] else ""))
+def test_splitkv_many_chunks(gpu_runner, case):
+    """Merges of 9 to 256 chunks, where the merge spreads a row's chunks over
+    2, 4 or 8 lane groups: decode (32-key tiles) and prefill (64-key tiles)
+    shapes, and causal rows that see only the first chunks, against the FP64
+    oracle with and without LSE."""
+    import torch
+    (b, h, sq, sk), causal = case
+    q, k, v = orc.make_inputs(b, h, sq, sk, "normal", seed=21)
+    ref, ref_lse = orc.attention_fp64(q, k, v, orc.DEFAULT_SCALE, causal)
+    for splits in (9, 17, 33, 100, 256):
+        for with_lse in (False, True):
+            o, lse = _run(gpu_runner, torch, q, k, v, causal, splits, with_lse)
+            e = orc.errors(o, lse, ref, ref_lse if with_lse else None)
+            assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (splits, with_lse, e)
