@@ -507,11 +507,23 @@ def main():
         o = torch.empty_like(q)
         for causal in (False, True):
             fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
+            check = None
+            if not args.no_check:
+                o.fill_(float("nan"))
+                torch.cuda.synchronize()
+                with torch.cuda.stream(stream):
+                    fn()
+                torch.cuda.synchronize()
+                check, _ = check_rows(torch, orc, q, k, v, o, causal, pairs)
+                if not orc.check_acceptance_tolerance(check):
+                    raise SystemExit(f"sampled-row check failed (S{n}, causal={causal}): {check}")
             sm = time_graph(torch, fn, args.steps, args.warmup, 2, stream)
             us = statistics.mean(sm)
             tf = orc.flops(b, h, n, n, causal) / us / 1e6
-            sweep[f"S{n}_{'causal' if causal else 'dense'}"] = dict(us=round(us, 2), tflops=round(tf, 1))
-            print(f"# sweep S{n} causal={causal}: {us:.1f} us, {tf:.1f} TFLOP/s", file=sys.stderr, flush=True)
+            sweep[f"S{n}_{'causal' if causal else 'dense'}"] = dict(us=round(us, 2), tflops=round(tf, 1),
+                                                                    check=check)
+            print(f"# sweep S{n} causal={causal}: {us:.1f} us, {tf:.1f} TFLOP/s check={check}", file=sys.stderr,
+                  flush=True)
 
     dense = results[False]
     clk = loaded_gfx_clock(torch, lambda: runner.call(q, k, v, o, None, False, args.config,
