@@ -93,31 +93,24 @@ struct LdsOffsets {
     uint32_t v[2][4];   // V^T operand: [first/second 4-key group][32-dim block]
 };
 
-// A 32-key block of tile `start` is visible to the wave holding rows
-// [qw, qw+32) unless it lies past the key length or entirely above the
-// causal diagonal.
-template <bool MASKED, bool CAUSAL>
-__device__ __forceinline__ bool block_active(int k0, int sk, int qw) {
-    return !MASKED || (k0 < sk && (!CAUSAL || k0 <= qw + 31));
-}
-
 // S^T = K.Q^T for one tile: 8 MFMAs per 32-key block, K operands read ahead.
-template <int BN, bool MASKED, bool CAUSAL>
+// Masked tiles compute every block too (no branch around blocks past the key
+// length or above the diagonal): tile_mask then hides them, and the tile
+// stays one basic block for the scheduler.  K rows past sk hold zeros (the
+// DMA's bounded buffer returns 0 there), so those scores are finite.
+template <int BN>
 __device__ __forceinline__ void tile_qk(const unsigned char* ks, const LdsOffsets& off, const bf16x8 (&qr)[8],
-                                        f32x16 (&s)[BN / 32], int start, int sk, int qw) {
+                                        f32x16 (&s)[BN / 32]) {
     constexpr int KB = BN / 32;
     const f32x16 zero = {};
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-        s[kb] = zero;
-        if (block_active<MASKED, CAUSAL>(start + kb * 32, sk, qw)) {
-            bf16x8 kop[8];
+        bf16x8 kop[8];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) kop[c] = lds_read16(ks + kb * 32 * ROW_BYTES + off.k[c]);
-            s[kb] = mfma32(kop[0], qr[0], zero);
+        for (int c = 0; c < 8; ++c) kop[c] = lds_read16(ks + kb * 32 * ROW_BYTES + off.k[c]);
+        s[kb] = mfma32(kop[0], qr[0], zero);
 #pragma unroll
-            for (int c = 1; c < 8; ++c) s[kb] = mfma32(kop[c], qr[c], s[kb]);
-        }
+        for (int c = 1; c < 8; ++c) s[kb] = mfma32(kop[c], qr[c], s[kb]);
     }
 }
 
@@ -130,23 +123,19 @@ struct SmCarry {
     bool rescale;     // some lane of the wave moved its base: O must be rescaled
 };
 
-// Masks of one tile (diagonal / tail variant only).
+// Masks of one tile (diagonal / tail variant only): a score is -inf past the
+// key length or above the causal diagonal, one select per score and no branch.
 template <int BN, bool MASKED, bool CAUSAL>
-__device__ __forceinline__ void tile_mask(f32x16 (&s)[BN / 32], int start, int sk, int qw, int row, int half) {
+__device__ __forceinline__ void tile_mask(f32x16 (&s)[BN / 32], int start, int sk, int row, int half) {
     if constexpr (MASKED) {
+        const int lim = CAUSAL ? min(sk - 1, row) : sk - 1;   // last visible key of this row
 #pragma unroll
         for (int kb = 0; kb < BN / 32; ++kb) {
-            const int k0 = start + kb * 32;
-            if (!block_active<MASKED, CAUSAL>(k0, sk, qw)) {
+            const int kl = start + kb * 32 + half * 4;
 #pragma unroll
-                for (int v = 0; v < 16; ++v) s[kb][v] = -__builtin_inff();
-            } else if (k0 + 32 > sk || (CAUSAL && k0 + 31 > qw)) {
-                const int kl = k0 + half * 4;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int key = kl + (v >> 2) * 8 + (v & 3);
-                    if (key >= sk || (CAUSAL && key > row)) s[kb][v] = -__builtin_inff();
-                }
+            for (int v = 0; v < 16; ++v) {
+                const int key = kl + (v >> 2) * 8 + (v & 3);
+                s[kb][v] = key > lim ? -__builtin_inff() : s[kb][v];
             }
         }
     }
@@ -210,10 +199,10 @@ __device__ __forceinline__ float tile_rowmax(const f32x16 (&s)[BN / 32]) {
 // computed against 0 instead, so they come out 0 rather than NaN.
 template <int BN, bool MASKED, bool CAUSAL, bool LSE, bool EMPTY = false>
 __device__ __forceinline__ void attend_tail(f32x16 (&s)[BN / 32], const unsigned char* vs, const LdsOffsets& off,
-                                            RowState& st, bool first, int start, int sk, int qw, int row, int half,
+                                            RowState& st, bool first, int start, int sk, int row, int half,
                                             float scale2) {
     constexpr int KB = BN / 32, U = 2 * KB;
-    tile_mask<BN, MASKED, CAUSAL>(s, start, sk, qw, row, half);
+    tile_mask<BN, MASKED, CAUSAL>(s, start, sk, row, half);
     const float mx = tile_rowmax<BN>(s);
     const float cand = fmaxf(st.m, mx * scale2);
     const bool update = first || cand > st.m + RESCALE_THRESHOLD;
@@ -258,12 +247,12 @@ __device__ __forceinline__ void attend_tail(f32x16 (&s)[BN / 32], const unsigned
 template <int BN, bool MASKED, bool CAUSAL, bool LSE, bool EMPTY = false>
 __device__ __forceinline__ void attend_fused(const unsigned char* ks, const unsigned char* vs, const LdsOffsets& off,
                                              const bf16x8 (&qr)[8], RowState& st, bool first, int start, int sk,
-                                             int qw, int row, int half, float scale2) {
+                                             int row, int half, float scale2) {
     f32x16 s[BN / 32];
     __builtin_amdgcn_s_setprio(1);
-    tile_qk<BN, MASKED, CAUSAL>(ks, off, qr, s, start, sk, qw);
+    tile_qk<BN>(ks, off, qr, s);
     __builtin_amdgcn_s_setprio(0);
-    attend_tail<BN, MASKED, CAUSAL, LSE, EMPTY>(s, vs, off, st, first, start, sk, qw, row, half, scale2);
+    attend_tail<BN, MASKED, CAUSAL, LSE, EMPTY>(s, vs, off, st, first, start, sk, row, half, scale2);
 }
 
 // Base update from a precomputed row max, then all of the tile's P units and
@@ -425,7 +414,7 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
             // A causal tile entirely above this wave's rows changes nothing
             // (tile 0 never is): the wave only keeps the DMA and barriers.
             if (!(MASKED && CAUSAL) || t * BN <= qw + 31)
-                attend_fused<BN, MASKED, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st, t == 0, t * BN, a.sk, qw,
+                attend_fused<BN, MASKED, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st, t == 0, t * BN, a.sk,
                                                       row, half, scale2);
         };
         using S0 = std::integral_constant<int, 0>;
@@ -441,7 +430,7 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
                 SmCarry c;
                 wait_vmem();
                 __syncthreads();
-                tile_qk<BN, false, CAUSAL>(smem, off, qr, sa, 0, a.sk, qw);
+                tile_qk<BN>(smem, off, qr, sa);
                 float mx = tile_rowmax<BN>(sa);
                 // Pipelined tile t (stage STAGE = t%3): S(t) in `cur`, QK^T(t+1)
                 // into `nxt` from stage (t+1)%3, then PV(t).
@@ -453,7 +442,7 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
                     __syncthreads();
                     issue(t + 2);
                     __builtin_amdgcn_s_setprio(1);
-                    tile_qk<BN, false, CAUSAL>(ahead, off, qr, nxt, (t + 1) * BN, a.sk, qw);
+                    tile_qk<BN>(ahead, off, qr, nxt);
                     __builtin_amdgcn_s_setprio(0);
                     softmax_from_max<BN, LSE>(cur, mx, p, st, c, t == 0, scale2);
                     apply_rescale(st, c);
@@ -488,7 +477,7 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
                     __syncthreads();
                     issue(t + 1);
                     attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st,
-                                                                             t == 0, t * BN, a.sk, qw, row, half,
+                                                                             t == 0, t * BN, a.sk, row, half,
                                                                              scale2);
                 };
                 using M0 = std::integral_constant<int, 0>;
@@ -711,7 +700,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
                 const unsigned char* cur = smem + STAGE * STAGE_BYTES;
                 sync_and_prefetch(t);
                 attend_fused<BN, decltype(masked_c)::value, CAUSAL, true, CAUSAL>(
-                    cur, cur + TILE_BYTES, off, qr, st, t == t0, t * BN, a.sk, qw, row, half, scale2);
+                    cur, cur + TILE_BYTES, off, qr, st, t == t0, t * BN, a.sk, row, half, scale2);
             };
             using S0 = std::integral_constant<int, 0>;
             using S1 = std::integral_constant<int, 1>;
@@ -893,7 +882,7 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
                 // A causal tile entirely above this wave's rows changes nothing.
                 if (!(decltype(masked_c)::value && CAUSAL) || t * BN <= qw + 31)
                     attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st,
-                                                                           t == 0, t * BN, sk, qw, row, half, scale2);
+                                                                           t == 0, t * BN, sk, row, half, scale2);
             };
             using S0 = std::integral_constant<int, 0>;
             using S1 = std::integral_constant<int, 1>;
