@@ -169,12 +169,19 @@ int launch_split(const Fav4Args& a, const SplitPlan& p, void* ws, hipStream_t st
     sp.splits = p.splits;
     sp.tps = p.tps;
     const int grid = int(total < MAX_GRID ? total : MAX_GRID);
-    if (p.shape.bm == 32)
-        hipLaunchKernelGGL((fav4::fwd_kernel_split<32, CAUSAL, 1>), dim3(grid), dim3(64), 0, stream, a, sp, a.heads,
-                           tiles, int(total));
+    // The FP32 sums only feed an LSE output.
+    if (p.shape.bm == 32 && a.lse)
+        hipLaunchKernelGGL((fav4::fwd_kernel_split<32, CAUSAL, 1, true>), dim3(grid), dim3(64), 0, stream, a, sp,
+                           a.heads, tiles, int(total));
+    else if (p.shape.bm == 32)
+        hipLaunchKernelGGL((fav4::fwd_kernel_split<32, CAUSAL, 1, false>), dim3(grid), dim3(64), 0, stream, a, sp,
+                           a.heads, tiles, int(total));
+    else if (a.lse)
+        hipLaunchKernelGGL((fav4::fwd_kernel_split<64, CAUSAL, 8, true>), dim3(grid), dim3(512), 0, stream, a, sp,
+                           a.heads, tiles, int(total));
     else
-        hipLaunchKernelGGL((fav4::fwd_kernel_split<64, CAUSAL, 8>), dim3(grid), dim3(512), 0, stream, a, sp, a.heads,
-                           tiles, int(total));
+        hipLaunchKernelGGL((fav4::fwd_kernel_split<64, CAUSAL, 8, false>), dim3(grid), dim3(512), 0, stream, a, sp,
+                           a.heads, tiles, int(total));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // Lane groups per merged row: one per 8 chunks, at most 8 (one workgroup).

@@ -586,7 +586,9 @@ struct SplitArgs {
 // WAVES = 8, BN = 64: long-key prefill chunks (256-row q tiles).  WAVES = 1,
 // BN = 32: decode (sq <= 32): one wave per workgroup and 48 KiB of LDS, so
 // three workgroups share a CU and every resident wave computes.
-template <int BN, bool CAUSAL, int WAVES = 8>
+// LSE: keep the FP32 sums for the LSE output; without it the second log-sum
+// repeats the first (the merge reads it only when writing an LSE).
+template <int BN, bool CAUSAL, int WAVES, bool LSE>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int total) {
     constexpr int BM = WAVES * 32, STAGES = 3;
@@ -699,7 +701,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
                 constexpr int STAGE = decltype(stage_c)::value;
                 const unsigned char* cur = smem + STAGE * STAGE_BYTES;
                 sync_and_prefetch(t);
-                attend_fused<BN, decltype(masked_c)::value, CAUSAL, true, CAUSAL>(
+                attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE, CAUSAL>(
                     cur, cur + TILE_BYTES, off, qr, st, t == t0, t * BN, a.sk, row, half, scale2);
             };
             using S0 = std::integral_constant<int, 0>;
@@ -742,8 +744,9 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
         }
         if (half == 0 && row < a.sq) {
             float* lp = sp.lse_part + ((int64_t(split) * bhs + bh) * a.sq + row) * 2;
-            lp[0] = st.m + __builtin_amdgcn_logf(st.lb);
-            lp[1] = st.m + __builtin_amdgcn_logf(st.l);
+            const float sb = st.m + __builtin_amdgcn_logf(st.lb);
+            lp[0] = sb;
+            lp[1] = LSE ? st.m + __builtin_amdgcn_logf(st.l) : sb;
         }
         wait_vmem();
         __syncthreads();
