@@ -43,6 +43,7 @@ sys.path.insert(0, str(ROOT))
 PEAK_BF16_TFLOPS = 2516.6      # MI355X dense BF16 MFMA: 256 CU x 4 SIMD x 1024 FLOP/clk x 2.4 GHz
 HBM_TBPS = 8.0
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_fmha_fwd_dense_b32h8s4096.md"
+SWEEP_SPIN_MS = 50.0           # untimed spin-up before each sweep shape (report-only rows)
 
 
 def parse_args():
@@ -116,8 +117,12 @@ def check_rows(torch, orc, q, k, v, o, causal, pairs):
     return orc.errors(sel_got, None, sel_ref, None), rows
 
 
-def time_graph(torch, fn, steps, warmup, observations, stream):
-    """Per-launch microseconds from HIP-graph replays bracketed by events on `stream`."""
+def time_graph(torch, fn, steps, warmup, observations, stream, spin_ms=0.0):
+    """Per-launch microseconds from HIP-graph replays bracketed by events on `stream`.
+
+    spin_ms > 0: before the observations, replay the warmup graph (untimed)
+    until that much wall time has passed, so that short launches are timed at
+    the loaded clock rather than while the GPU ramps up from idle."""
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         g_timed = torch.cuda.CUDAGraph()
@@ -128,6 +133,12 @@ def time_graph(torch, fn, steps, warmup, observations, stream):
         with torch.cuda.graph(g_warm, stream=stream):
             for _ in range(warmup):
                 fn()
+    if spin_ms > 0:
+        t_end = time.perf_counter() + spin_ms / 1000.0
+        while time.perf_counter() < t_end:
+            with torch.cuda.stream(stream):
+                g_warm.replay()
+            torch.cuda.synchronize()
     samples = []
     for _ in range(observations):
         with torch.cuda.stream(stream):
@@ -517,7 +528,7 @@ def main():
                 check, _ = check_rows(torch, orc, q, k, v, o, causal, pairs)
                 if not orc.check_acceptance_tolerance(check):
                     raise SystemExit(f"sampled-row check failed (S{n}, causal={causal}): {check}")
-            sm = time_graph(torch, fn, args.steps, args.warmup, 2, stream)
+            sm = time_graph(torch, fn, args.steps, args.warmup, 2, stream, spin_ms=SWEEP_SPIN_MS)
             us = statistics.mean(sm)
             tf = orc.flops(b, h, n, n, causal) / us / 1e6
             sweep[f"S{n}_{'causal' if causal else 'dense'}"] = dict(us=round(us, 2), tflops=round(tf, 1),

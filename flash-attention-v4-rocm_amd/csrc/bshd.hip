@@ -197,11 +197,15 @@ int launch_split(const Fav4Args& a, const SplitPlan& p, void* ws, hipStream_t st
 
 }  // namespace
 
-// Replaces src/bshd.hip:23-25.  Small query lengths use 128-row workgroups so
-// short sequences still spread over the 256 CUs; everything else uses 256 rows.
+// Replaces src/bshd.hip:23-25.  Query lengths up to 1024 use 128-row
+// workgroups (two per CU, so one's prologue and epilogue overlap the other's
+// key loop, and small grids spread over more CUs); longer ones use 256 rows.
+// Measured on MI355X at B32 H8 and B4 H8, dense and causal: config 1 is
+// faster or equal up to Sq 896, and at Sq 1024 loses 1.4% dense while gaining
+// 4% causal; from Sq 1536 (B32) config 2 wins dense.
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_select_config(const Fav4Args* a) {
     if (!a) return -1;
-    return a->sq < 256 ? 1 : 2;
+    return a->sq <= 1024 ? 1 : 2;
 }
 
 // Replaces src/bshd.hip:26-38.

@@ -30,8 +30,8 @@ struct Fav4Args {
 // Config IDs (gfx950 tile shapes; BM = query rows per workgroup, BN = keys per
 // K/V tile, 32 query rows per wave64):
 //  0: Auto (fav4_bshd_select_config)
-//  1: BM 128 / BN 64, 4 waves, 2 LDS stages  -- short query lengths, small grids
-//  2: BM 256 / BN 64, 8 waves, 2 LDS stages  -- default for sq >= 256
+//  1: BM 128 / BN 64, 4 waves, 2 LDS stages  -- Auto for sq <= 1024
+//  2: BM 256 / BN 64, 8 waves, 2 LDS stages  -- Auto for sq > 1024
 //  3: BM 256 / BN 64, 8 waves, 3 LDS stages with QK^T(t+1) pipelined
 //     beside softmax(t)
 //

@@ -114,7 +114,8 @@ def test_rejects_null_args(lib):
     assert lib.fav4_bshd_select_config(None) == -1
 
 
-@pytest.mark.parametrize("sq,want", [(1, 1), (127, 1), (255, 1), (256, 2), (1000, 2), (4096, 2), (32768, 2)])
+@pytest.mark.parametrize("sq,want", [(1, 1), (127, 1), (256, 1), (1000, 1), (1024, 1), (1025, 2), (4096, 2),
+                                     (32768, 2)])
 def test_select_config(lib, Args, sq, want):
     fields = _good(Args)
     fields["sq"] = sq
