@@ -195,17 +195,29 @@ int launch_split(const Fav4Args& a, const SplitPlan& p, void* ws, hipStream_t st
     return hipGetLastError();
 }
 
+// Auto: 128-row workgroups (config 1; two per CU, so one's prologue and
+// epilogue overlap the other's key loop) for query lengths up to 1024, and
+// wherever 256-row workgroups (config 2) would leave CUs without a work item
+// (items: q tiles; causal: q-tile pairs); else config 2.  Measured on MI355X
+// (graph-timed, config 1 vs 2): up to Sq 896 config 1 is faster or equal at
+// B32 and B4 H8, at Sq 1024 it loses 1.4% dense and gains 4% causal; with
+// fewer config-2 items than CUs it wins by 28-46% (B1 H8 S2048..S4096, causal
+// B1 H8 S8192, B2 H8 S4096); with one item per CU or more config 2 wins by
+// 6-8% (dense B2 H8 S4096, B1 H32 S4096, causal B1 H32 S4096).
+int auto_config(const Fav4Args& a, int causal) {
+    if (a.sq <= 1024) return 1;
+    const int64_t tiles = (int64_t(a.sq) + 255) / 256;
+    const int64_t items = int64_t(a.batch) * a.heads * (causal ? (tiles + 1) / 2 : tiles);
+    return items < device_cus() ? 1 : 2;
+}
+
 }  // namespace
 
-// Replaces src/bshd.hip:23-25.  Query lengths up to 1024 use 128-row
-// workgroups (two per CU, so one's prologue and epilogue overlap the other's
-// key loop, and small grids spread over more CUs); longer ones use 256 rows.
-// Measured on MI355X at B32 H8 and B4 H8, dense and causal: config 1 is
-// faster or equal up to Sq 896, and at Sq 1024 loses 1.4% dense while gaining
-// 4% causal; from Sq 1536 (B32) config 2 wins dense.
+// Replaces src/bshd.hip:23-25 (the dense choice; the forward calls
+// auto_config with its mask).
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_select_config(const Fav4Args* a) {
     if (!a) return -1;
-    return a->sq <= 1024 ? 1 : 2;
+    return auto_config(*a, 0);
 }
 
 // Replaces src/bshd.hip:26-38.
@@ -213,7 +225,7 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward(const Fa
                                                                 hipStream_t stream) {
     const int st = validate(a, causal, config);
     if (st != hipSuccess) return st;
-    if (config == 0) config = fav4_bshd_select_config(a);
+    if (config == 0) config = auto_config(*a, causal);
     const fav4::Layout L = bshd_layout(*a, a->heads);
     return causal ? dispatch<true>(*a, L, config, stream) : dispatch<false>(*a, L, config, stream);
 }
@@ -237,7 +249,7 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_strided(
     L.vb = v->batch * 2; L.vh = v->head * 2; L.vr = uint32_t(v->seq * 2);
     L.ob = o->batch * 2; L.oh = o->head * 2; L.orow = uint32_t(o->seq * 2);
     L.group = a->heads / kv_heads;
-    if (config == 0) config = fav4_bshd_select_config(a);
+    if (config == 0) config = auto_config(*a, causal);
     return causal ? dispatch<true>(*a, L, config, stream) : dispatch<false>(*a, L, config, stream);
 }
 
@@ -277,7 +289,7 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_gqa(cons
     const int st = validate(a, causal, config);
     if (st != hipSuccess) return st;
     if (kv_heads <= 0 || kv_heads > a->heads || a->heads % kv_heads != 0) return hipErrorInvalidValue;
-    if (config == 0) config = fav4_bshd_select_config(a);
+    if (config == 0) config = auto_config(*a, causal);
     const fav4::Layout L = bshd_layout(*a, kv_heads);
     return causal ? dispatch<true>(*a, L, config, stream) : dispatch<false>(*a, L, config, stream);
 }

@@ -29,16 +29,20 @@ struct Fav4Args {
 //
 // Config IDs (gfx950 tile shapes; BM = query rows per workgroup, BN = keys per
 // K/V tile, 32 query rows per wave64):
-//  0: Auto (fav4_bshd_select_config)
-//  1: BM 128 / BN 64, 4 waves, 2 LDS stages  -- Auto for sq <= 1024
-//  2: BM 256 / BN 64, 8 waves, 2 LDS stages  -- Auto for sq > 1024
+//  0: Auto: config 1 for sq <= 1024 or when config 2 would have fewer work
+//     items than the device has CUs (items: B*H*ceil(sq/256) q tiles; causal:
+//     B*H*ceil(ceil(sq/256)/2) q-tile pairs), else config 2
+//  1: BM 128 / BN 64, 4 waves, 2 LDS stages
+//  2: BM 256 / BN 64, 8 waves, 2 LDS stages
 //  3: BM 256 / BN 64, 8 waves, 3 LDS stages with QK^T(t+1) pipelined
 //     beside softmax(t)
 //
 // Replaces include/fav4_bshd.h:19 (fav4_bshd_forward).
 extern "C" int fav4_bshd_forward(const Fav4Args* args, int causal, int config, hipStream_t stream);
 // Replaces include/fav4_bshd.h:20 (fav4_bshd_select_config): the config ID
-// that config 0 resolves to for these arguments (-1 for a NULL pointer).
+// that config 0 resolves to for these arguments in a dense call (the mask is
+// not an argument here; a causal call counts q-tile pairs, see above), -1 for
+// a NULL pointer.
 extern "C" int fav4_bshd_select_config(const Fav4Args* args);
 
 // ---- Split-KV forward --------------------------------------------------------

@@ -114,11 +114,16 @@ def test_rejects_null_args(lib):
     assert lib.fav4_bshd_select_config(None) == -1
 
 
-@pytest.mark.parametrize("sq,want", [(1, 1), (127, 1), (256, 1), (1000, 1), (1024, 1), (1025, 2), (4096, 2),
-                                     (32768, 2)])
-def test_select_config(lib, Args, sq, want):
+@pytest.mark.parametrize("b,h,sq,want", [
+    (2, 4, 1, 1), (2, 4, 127, 1), (32, 8, 256, 1), (32, 8, 1000, 1), (32, 8, 1024, 1),   # Sq <= 1024: config 1
+    (32, 8, 1025, 2), (32, 8, 4096, 2), (32, 8, 32768, 2), (2, 8, 4096, 2), (1, 32, 4096, 2),
+    (1, 8, 4096, 1), (1, 8, 8192, 2), (2, 4, 4096, 1), (1, 1, 32768, 1)])   # fewer q tiles than 256 CUs: config 1
+def test_select_config(lib, Args, b, h, sq, want):
+    """Closed form of Auto for a dense call on 256 CUs (the library's value
+    when no device is visible): config 1 for Sq <= 1024 or fewer than 256
+    q tiles of 256 rows, else config 2."""
     fields = _good(Args)
-    fields["sq"] = sq
+    fields.update(batch=b, heads=h, sq=sq)
     got = lib.fav4_bshd_select_config(C.byref(Args(**fields)))
     assert got == want and 1 <= got <= 3
 
