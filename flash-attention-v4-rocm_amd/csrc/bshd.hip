@@ -195,6 +195,19 @@ int launch_split(const Fav4Args& a, const SplitPlan& p, void* ws, hipStream_t st
     return hipGetLastError();
 }
 
+template <int WAVES>
+void launch_varlen(const Fav4VarlenArgs& a, int causal, int tiles, int total, int grid, hipStream_t stream) {
+    const dim3 block(WAVES * 64);
+    if (causal && a.lse)
+        hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, true, true, WAVES>), dim3(grid), block, 0, stream, a, tiles, total);
+    else if (causal)
+        hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, true, false, WAVES>), dim3(grid), block, 0, stream, a, tiles, total);
+    else if (a.lse)
+        hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, false, true, WAVES>), dim3(grid), block, 0, stream, a, tiles, total);
+    else
+        hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, false, false, WAVES>), dim3(grid), block, 0, stream, a, tiles, total);
+}
+
 // Auto: 128-row workgroups (config 1; two per CU, so one's prologue and
 // epilogue overlap the other's key loop) for query lengths up to 1024, and
 // wherever 256-row workgroups (config 2) would leave CUs without a work item
@@ -269,17 +282,20 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_varlen(c
         ((reinterpret_cast<uintptr_t>(a->cu_seqlens_q) | reinterpret_cast<uintptr_t>(a->cu_seqlens_k)) & 3) ||
         (a->lse && (reinterpret_cast<uintptr_t>(a->lse) & 3)))
         return hipErrorInvalidValue;
-    const int tiles = (a->max_seqlen_q + 255) / 256;
+    // The forward's Auto rule on the longest sequence: 128-row tiles (4 waves)
+    // for max_seqlen_q <= 1024 or when 256-row tiles would give fewer
+    // (sequence, head, q tile) items than CUs; else 256-row tiles.
+    const int64_t tiles256 = (int64_t(a->max_seqlen_q) + 255) / 256;
+    const bool small = a->max_seqlen_q <= 1024 || int64_t(a->batch) * a->heads * tiles256 < device_cus();
+    const int bm = small ? 128 : 256;
+    const int tiles = (a->max_seqlen_q + bm - 1) / bm;
     const int64_t total = int64_t(a->batch) * a->heads * tiles;
     if (total > INT_MAX) return hipErrorInvalidValue;
     const int grid = int(total < MAX_GRID ? total : MAX_GRID);
-    if (causal) {
-        if (a->lse) hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, true, true>), dim3(grid), dim3(512), 0, stream, *a, tiles, int(total));
-        else hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, true, false>), dim3(grid), dim3(512), 0, stream, *a, tiles, int(total));
-    } else {
-        if (a->lse) hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, false, true>), dim3(grid), dim3(512), 0, stream, *a, tiles, int(total));
-        else hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, false, false>), dim3(grid), dim3(512), 0, stream, *a, tiles, int(total));
-    }
+    if (small)
+        launch_varlen<4>(*a, causal, tiles, int(total), grid, stream);
+    else
+        launch_varlen<8>(*a, causal, tiles, int(total), grid, stream);
     return hipGetLastError();
 }
 

@@ -762,10 +762,10 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
 // offsets read from device memory are clamped to [0, total] and to the
 // maximum lengths, so every access stays inside the caller's buffers.
 // ---------------------------------------------------------------------------
-template <int BN, bool CAUSAL, bool LSE>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int BN, bool CAUSAL, bool LSE, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
-    constexpr int WAVES = 8, BM = 256;
+    constexpr int BM = WAVES * 32;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
     constexpr int STAGE_BYTES = 2 * TILE_BYTES;
     constexpr int DMA = BN / 4 / WAVES;

@@ -56,6 +56,29 @@ def test_headline_b32h8s4096_all_configs(gpu_runner, causal):
 
 
 @pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
+@pytest.mark.parametrize("shape", [(2, 4, 1000, 1500), (1, 2, 257, 3000), (3, 1, 64, 64), (1, 8, 4096, 4096)],
+                         ids=lambda s: "b%dh%d_%dx%d" % s)
+def test_configs_1_and_2_bitwise(gpu_runner, shape, causal):
+    """128-row (config 1) and 256-row (config 2) workgroups run the same
+    per-wave tile loop over the same 64-key tiles, so every row's O and LSE
+    are bitwise equal: Auto may pick either, and the varlen kernel (which
+    follows the same choice) matches the forward at any config."""
+    import torch
+    b, h, sq, sk = shape
+    q, k, v = _gpu_inputs(torch, b, h, sq, sk)
+    outs = []
+    for config in (1, 2):
+        o = torch.full_like(q, float("nan"))
+        lse = torch.full((b, h, sq), float("nan"), device="cuda", dtype=torch.float32)
+        print(f"  config {config} B{b} H{h} {sq}x{sk} causal={causal}", flush=True)
+        gpu_runner.call(q, k, v, o, lse, causal, config)
+        torch.cuda.synchronize()
+        outs.append((o, lse))
+    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
+    assert torch.equal(outs[0][1].view(torch.int32), outs[1][1].view(torch.int32))
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
 @pytest.mark.parametrize("shape", [(8, 16, 2048, 2048), (8, 16, 1030, 1950)], ids=["even_tiles", "odd_tiles"])
 def test_slices_match_isolated_launches(gpu_runner, shape, causal):
     """The result of a (b, h) slice must not depend on the rest of the launch

@@ -4,8 +4,10 @@ Sequence b's query rows are [cu_q[b], cu_q[b+1]) of the packed Q/O and its
 key rows [cu_k[b], cu_k[b+1]) of the packed K/V.  Pins:
   * bitwise equality, sequence by sequence, with fav4_bshd_forward (MHA) or
     fav4_bshd_forward_gqa (GQA) at config 2 on that sequence alone: the varlen
-    kernel runs the same tile loop (8 waves, BM 256, BN 64, 2 LDS stages), so
-    any difference is an indexing error (wrong sequence, head or row);
+    kernel runs the same per-wave tile loop (BN 64, 2 LDS stages; 128-row
+    workgroups for max_seqlen_q <= 1024 or small grids, else 256-row ones,
+    both bitwise equal to config 2), so any difference is an indexing error
+    (wrong sequence, head or row);
   * the FP64 oracle on every sequence, at the reference harness's bar;
   * a sequence without keys gives O = 0 and LSE = -inf, one without queries
     writes nothing, and rows outside O / LSE are never written.
