@@ -324,8 +324,9 @@ def splitkv_report(torch, orc, runner, args, stream, b=1, h=8, sq=1024, sk=32768
 def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
     """The GQA and varlen entry points at the headline token count (B*S rows, H8):
     GQA with `kvh` K/V heads; varlen with B ragged sequences of seeded lengths in
-    [S/4, 7S/4].  Graph-timed, each output first checked against the FP64 oracle
-    on sampled rows of two (sequence, head) pairs of two sequences."""
+    [S/4, 7S/4]; and a GQA decode through split-KV.  Graph-timed, each output
+    first checked against the FP64 oracle on sampled rows of two (sequence,
+    head) pairs of two sequences."""
     g = torch.Generator(device="cuda")
     g.manual_seed(11939)
     mk = lambda *shape: torch.randn(shape, device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
@@ -374,6 +375,36 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
         res["causal" if causal else "dense"] = measure(f"varlen causal={causal}", fn, o, checks, flop)
     out["varlen"] = res
     del q, k, v, o
+    torch.cuda.empty_cache()
+
+    # GQA decode through split-KV: one query per sequence against a long
+    # cache; the query heads of a K/V head share its stream.  Reported as K+V
+    # bandwidth (the bound).
+    db, dh, dkvh, dsk = 4, 32, 8, 32768
+    q, k, v = mk(db, 1, dh, 128), mk(db, dsk, dkvh, 128), mk(db, dsk, dkvh, 128)
+    o = torch.empty_like(q)
+    need = runner.splitkv_workspace_size(db, dh, 1, dsk, False, 0, kv_heads=dkvh)
+    ws = torch.empty(max(need, 256), device="cuda", dtype=torch.uint8)
+    fn = lambda: runner.call_splitkv(q, k, v, o, None, False, 0, workspace=ws, stream=stream.cuda_stream)
+    o.fill_(float("nan"))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        fn()
+    torch.cuda.synchronize()
+    grp = dh // dkvh
+    for i in (0, db - 1):
+        err, _ = check_rows(torch, orc, q[i:i + 1], k[i:i + 1].repeat_interleave(grp, dim=2),
+                            v[i:i + 1].repeat_interleave(grp, dim=2), o[i:i + 1], False, [(0, 0), (0, dh - 1)])
+        if not orc.check_acceptance_tolerance(err):
+            raise SystemExit(f"api report: gqa decode check failed: {err}")
+    us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+    kv_bytes = 2 * db * dsk * dkvh * 256
+    splits = runner.splitkv_select(db, dh, 1, dsk, False, kv_heads=dkvh)
+    print(f"# gqa decode (split-KV, {splits} chunks): {us:.1f} us, K+V {kv_bytes / us / 1e6:.2f} TB/s",
+          file=sys.stderr, flush=True)
+    out["gqa_decode"] = {"workload": f"B{db} H{dh} KV heads {dkvh} Sq=1 Sk={dsk} D128 BF16 dense, split-KV Auto",
+                         "splits": splits, "us": round(us, 2), "kv_tbps": round(kv_bytes / us / 1e6, 2)}
+    del q, k, v, o, ws
     torch.cuda.empty_cache()
     return out
 

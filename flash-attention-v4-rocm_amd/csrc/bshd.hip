@@ -102,6 +102,8 @@ SplitShape split_shape(const Fav4Args& a) {
 struct SplitPlan {
     int splits, tps;   // chunks and key tiles per chunk
     SplitShape shape;
+    int tiles;         // q tiles per item
+    int64_t items;     // (batch, head) items, or (batch, K/V head) groups for decode
 };
 
 // CU count of the current device (256 if it cannot be read), cached per
@@ -122,20 +124,25 @@ int device_cus() {
 // shape's resident workgroups per CU; more chunks only add merge traffic and
 // per-chunk pipeline fill).  The count is then rounded so that no chunk
 // starts past that range.
-SplitPlan split_plan(const Fav4Args& a, int causal, int req) {
+// The decode shape packs the query heads that share a K/V head into one row
+// space of (heads / kv_heads) * sq rows per (batch, K/V head).
+SplitPlan split_plan(const Fav4Args& a, int kv_heads, int causal, int req) {
     const SplitShape sh = split_shape(a);
-    const int tiles = (a.sq + sh.bm - 1) / sh.bm;
+    const bool pack = sh.bm == 32;
+    const int rows = pack ? (a.heads / kv_heads) * a.sq : a.sq;
+    const int tiles = (rows + sh.bm - 1) / sh.bm;
+    const int64_t items = int64_t(a.batch) * (pack ? kv_heads : a.heads);
     const int keys = causal ? std::min(a.sk, a.sq) : a.sk;
     const int ktiles = (keys + sh.bn - 1) / sh.bn;
     int64_t splits = req;
     if (splits == 0) {
-        const int64_t items = int64_t(a.batch) * a.heads * tiles;
-        splits = (int64_t(device_cus()) * sh.wgs_per_cu + items - 1) / items;
+        const int64_t units = items * tiles;
+        splits = (int64_t(device_cus()) * sh.wgs_per_cu + units - 1) / units;
         splits = std::min<int64_t>(splits, std::min(sh.auto_max, std::max(1, ktiles / MIN_TILES_PER_SPLIT)));
     }
     splits = std::max<int64_t>(1, std::min<int64_t>(splits, ktiles));
     const int tps = int((ktiles + splits - 1) / splits);
-    return {(ktiles + tps - 1) / tps, tps, sh};
+    return {(ktiles + tps - 1) / tps, tps, sh, tiles, items};
 }
 
 int64_t split_workspace(const Fav4Args& a, const SplitPlan& p) {
@@ -144,23 +151,24 @@ int64_t split_workspace(const Fav4Args& a, const SplitPlan& p) {
 }
 
 // Shape-only checks for the split-KV queries (no buffers needed yet).
-int split_shape_ok(const Fav4Args* a, int causal, int splits) {
+int split_shape_ok(const Fav4Args* a, int kv_heads, int causal, int splits) {
     if (!a || a->batch <= 0 || a->heads <= 0 || a->sq <= 0 || a->sk <= 0 || (causal != 0 && causal != 1) ||
         a->batch > INT_MAX / a->heads || a->heads > INT_MAX / 128 || a->sq > INT_MAX / (a->heads * 128) ||
-        a->sk > INT_MAX / (a->heads * 128) || splits < 0 || splits > fav4::MAX_SPLITS || a->sq > MAX_SPLIT_SQ)
+        a->sk > INT_MAX / (a->heads * 128) || splits < 0 || splits > fav4::MAX_SPLITS || a->sq > MAX_SPLIT_SQ ||
+        kv_heads <= 0 || kv_heads > a->heads || a->heads % kv_heads != 0)
         return hipErrorInvalidValue;
     return hipSuccess;
 }
 
-int split_args_ok(const Fav4Args* a, int causal, int splits) {
+int split_args_ok(const Fav4Args* a, int kv_heads, int causal, int splits) {
     const int st = validate(a, causal, 0);
-    return st != hipSuccess ? st : split_shape_ok(a, causal, splits);
+    return st != hipSuccess ? st : split_shape_ok(a, kv_heads, causal, splits);
 }
 
 template <bool CAUSAL>
-int launch_split(const Fav4Args& a, const SplitPlan& p, void* ws, hipStream_t stream) {
-    const int tiles = (a.sq + p.shape.bm - 1) / p.shape.bm;
-    const int64_t total = int64_t(a.batch) * a.heads * tiles * p.splits;
+int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, hipStream_t stream) {
+    const int tiles = p.tiles;
+    const int64_t total = p.items * tiles * p.splits;
     const int64_t rows = int64_t(a.batch) * a.heads * a.sq;
     if (total > INT_MAX || rows > INT_MAX) return hipErrorInvalidValue;
     fav4::SplitArgs sp;
@@ -172,16 +180,16 @@ int launch_split(const Fav4Args& a, const SplitPlan& p, void* ws, hipStream_t st
     // The FP32 sums only feed an LSE output.
     if (p.shape.bm == 32 && a.lse)
         hipLaunchKernelGGL((fav4::fwd_kernel_split<32, CAUSAL, 1, true>), dim3(grid), dim3(64), 0, stream, a, sp,
-                           a.heads, tiles, int(total));
+                           kv_heads, tiles, int(total));
     else if (p.shape.bm == 32)
         hipLaunchKernelGGL((fav4::fwd_kernel_split<32, CAUSAL, 1, false>), dim3(grid), dim3(64), 0, stream, a, sp,
-                           a.heads, tiles, int(total));
+                           kv_heads, tiles, int(total));
     else if (a.lse)
         hipLaunchKernelGGL((fav4::fwd_kernel_split<64, CAUSAL, 8, true>), dim3(grid), dim3(512), 0, stream, a, sp,
-                           a.heads, tiles, int(total));
+                           kv_heads, tiles, int(total));
     else
         hipLaunchKernelGGL((fav4::fwd_kernel_split<64, CAUSAL, 8, false>), dim3(grid), dim3(512), 0, stream, a, sp,
-                           a.heads, tiles, int(total));
+                           kv_heads, tiles, int(total));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // Lane groups per merged row: one per 8 chunks, at most 8 (one workgroup).
@@ -311,27 +319,50 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_gqa(cons
 }
 
 // Split-KV entry points (no counterpart in the reference; see the header).
+// The MHA ones are the GQA ones with kv_heads = heads.
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_splitkv_gqa_select(const Fav4Args* a, int kv_heads,
+                                                                           int causal) {
+    if (split_shape_ok(a, kv_heads, causal, 0) != hipSuccess) return -1;
+    return split_plan(*a, kv_heads, causal, 0).splits;
+}
+
+extern "C" __attribute__((visibility("default"))) long long fav4_bshd_splitkv_gqa_workspace_size(const Fav4Args* a,
+                                                                                              int kv_heads,
+                                                                                              int causal,
+                                                                                              int splits) {
+    if (split_shape_ok(a, kv_heads, causal, splits) != hipSuccess) return -1;
+    return split_workspace(*a, split_plan(*a, kv_heads, causal, splits));
+}
+
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_gqa(const Fav4Args* a, int kv_heads,
+                                                                            int causal, int splits,
+                                                                            void* workspace,
+                                                                            size_t workspace_bytes,
+                                                                            hipStream_t stream) {
+    const int st = split_args_ok(a, kv_heads, causal, splits);
+    if (st != hipSuccess) return st;
+    const SplitPlan p = split_plan(*a, kv_heads, causal, splits);
+    if (p.splits == 1) return fav4_bshd_forward_gqa(a, kv_heads, causal, 0, stream);
+    const int64_t need = split_workspace(*a, p);
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || uint64_t(need) > workspace_bytes)
+        return hipErrorInvalidValue;
+    return causal ? launch_split<true>(*a, kv_heads, p, workspace, stream)
+                  : launch_split<false>(*a, kv_heads, p, workspace, stream);
+}
+
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_splitkv_select(const Fav4Args* a, int causal) {
-    if (split_shape_ok(a, causal, 0) != hipSuccess) return -1;
-    return split_plan(*a, causal, 0).splits;
+    return a ? fav4_bshd_splitkv_gqa_select(a, a->heads, causal) : -1;
 }
 
 extern "C" __attribute__((visibility("default"))) long long fav4_bshd_splitkv_workspace_size(const Fav4Args* a,
                                                                                           int causal, int splits) {
-    if (split_shape_ok(a, causal, splits) != hipSuccess) return -1;
-    return split_workspace(*a, split_plan(*a, causal, splits));
+    return a ? fav4_bshd_splitkv_gqa_workspace_size(a, a->heads, causal, splits) : -1;
 }
 
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv(const Fav4Args* a, int causal,
                                                                         int splits, void* workspace,
                                                                         size_t workspace_bytes,
                                                                         hipStream_t stream) {
-    const int st = split_args_ok(a, causal, splits);
-    if (st != hipSuccess) return st;
-    const SplitPlan p = split_plan(*a, causal, splits);
-    if (p.splits == 1) return fav4_bshd_forward(a, causal, 0, stream);
-    const int64_t need = split_workspace(*a, p);
-    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || uint64_t(need) > workspace_bytes)
-        return hipErrorInvalidValue;
-    return causal ? launch_split<true>(*a, p, workspace, stream) : launch_split<false>(*a, p, workspace, stream);
+    if (!a) return hipErrorInvalidValue;
+    return fav4_bshd_forward_splitkv_gqa(a, a->heads, causal, splits, workspace, workspace_bytes, stream);
 }

@@ -592,6 +592,11 @@ template <int BN, bool CAUSAL, int WAVES, bool LSE>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int total) {
     constexpr int BM = WAVES * 32, STAGES = 3;
+    // One wave (decode): the q-tile rows are the group's query heads times
+    // their sq queries, row r = (head - first head of the group) * sq + query,
+    // so the heads that share a K/V head stream it once.  Eight waves: the
+    // rows of one head.
+    constexpr bool PACK = WAVES == 1;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
     constexpr int STAGE_BYTES = 2 * TILE_BYTES;
     constexpr int DMA = BN / 4 / WAVES;
@@ -630,31 +635,46 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
         dv[i] = r * kv_row_bytes + ((p ^ v_swz(r)) << 4);
     }
 
+    // Rows of one item's row space: a head's queries, or a group's.
+    const int rows = PACK ? group * a.sq : a.sq;
     for (int id = blockIdx.x; id < total; id += gridDim.x) {
-        // XCD-contiguous order; within a (b, h) the q tiles of one key chunk
-        // are adjacent, so they share that chunk in L2.
+        // XCD-contiguous order; within a (b, h) -- PACK: (b, K/V head) -- the
+        // q tiles of one key chunk are adjacent, so they share it in L2.
         const int xcd = id & 7, slot = id >> 3, per = total >> 3, rem = total & 7;
         const int logical = xcd * per + min(xcd, rem) + slot;
-        const int per_bh = tiles * sp.splits;
-        const int bh = __builtin_amdgcn_readfirstlane(logical / per_bh);
-        const int r = __builtin_amdgcn_readfirstlane(logical - bh * per_bh);
+        const int per_item = tiles * sp.splits;
+        const int it = __builtin_amdgcn_readfirstlane(logical / per_item);
+        const int r = __builtin_amdgcn_readfirstlane(logical - it * per_item);
         const int split = r / tiles, tile = r - split * tiles;
 
-        const int batch = bh / a.heads, head = bh - batch * a.heads;
+        // it = b*heads + h, or (PACK) b*kv_heads + K/V head; head0 = the first
+        // query head of the item's rows.
+        const int items_per_batch = PACK ? kv_heads : a.heads;
+        const int batch = it / items_per_batch, unit = it - batch * items_per_batch;
+        const int head0 = PACK ? unit * group : unit;
+        const int bh = batch * a.heads + head0;
         const int q0 = tile * BM, qw = q0 + wave * 32;
-        const int row = qw + col;
-        const int64_t qrow0 = (int64_t(batch) * a.sq + q0) * a.heads + head;
-        const int64_t krow0 = int64_t(batch) * a.sk * kv_heads + head / group;
+        const int row = qw + col;                              // row of the item's row space
+        // This lane's query position (causal limit) and Q byte offset inside
+        // the batch's [sq, heads] block; rows past the space read a valid row.
+        const int prow = min(row, rows - 1);
+        const int qi = PACK ? prow % a.sq : prow;
+        const int qhead = PACK ? head0 + prow / a.sq : head0;
+        const int64_t krow0 = int64_t(batch) * a.sk * kv_heads + head0 / group;
         const char* kbase = static_cast<const char*>(a.k) + krow0 * ROW_BYTES;
         const char* vbase = static_cast<const char*>(a.v) + krow0 * ROW_BYTES;
-        const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + qrow0 * ROW_BYTES,
-                                    uint32_t(a.sq - q0 - 1) * row_bytes + ROW_BYTES);
-        // This chunk's rows of o_part: [sq - q0 rows][128] FP32 from row q0.
+        const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + int64_t(batch) * a.sq * row_bytes,
+                                    uint32_t(a.sq) * row_bytes);
+        // This chunk's rows of o_part: [rows - q0][128] FP32 from row q0 (a
+        // group's heads are adjacent, so its rows are contiguous).
         const int64_t prow0 = (int64_t(split) * bhs + bh) * a.sq + q0;
-        const rsrc_t rp = make_rsrc(sp.o_part + prow0 * D, uint32_t(a.sq - q0) * D * 4);
-        const int kend = CAUSAL ? min(a.sk, q0 + BM) : a.sk;
+        const rsrc_t rp = make_rsrc(sp.o_part + prow0 * D, uint32_t(rows - q0) * D * 4);
+        // PACK: every q tile holds rows of query 0 and of the last query, so
+        // the causal range is the whole [0, min(sk, sq)) and no tile is
+        // unmasked for every row.
+        const int kend = CAUSAL ? min(a.sk, PACK ? a.sq : q0 + BM) : a.sk;
         const int ntiles = (kend + BN - 1) / BN;
-        const int nfull = (CAUSAL ? min(a.sk, q0 + 1) : a.sk) / BN;
+        const int nfull = (CAUSAL ? (PACK ? 0 : min(a.sk, q0 + 1)) : a.sk) / BN;
         const int t0 = split * sp.tps, t1 = min(ntiles, t0 + sp.tps);
 
         RowState st;
@@ -684,7 +704,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
             issue(t0 + 1);
             bf16x8 qr[8];
             {
-                const uint32_t qoff = uint32_t(wave * 32 + col) * row_bytes + half * 16;
+                const uint32_t qoff = uint32_t(qi) * row_bytes + uint32_t(qhead) * ROW_BYTES + half * 16;
 #pragma unroll
                 for (int c = 0; c < 8; ++c) qr[c] = load16(rq, qoff + c * 32);
 #pragma unroll
@@ -702,7 +722,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
                 const unsigned char* cur = smem + STAGE * STAGE_BYTES;
                 sync_and_prefetch(t);
                 attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE, CAUSAL>(
-                    cur, cur + TILE_BYTES, off, qr, st, t == t0, t * BN, a.sk, row, half, scale2);
+                    cur, cur + TILE_BYTES, off, qr, st, t == t0, t * BN, a.sk, qi, half, scale2);
             };
             using S0 = std::integral_constant<int, 0>;
             using S1 = std::integral_constant<int, 1>;
@@ -711,7 +731,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
             using Masked = std::integral_constant<bool, true>;
             int t = t0;
             const int tp = min(t1, nfull);
-            if (qw >= a.sq) {
+            if (qw >= rows) {
                 // Rows all past sq (decode: 7 of 8 waves): only the DMA and
                 // barrier sequence of the loop below.
                 for (; t < t1; ++t) sync_and_prefetch(t);
@@ -742,7 +762,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
                 store16(rp, pbase + (db * 32 + vg * 8) * 4, x);
             }
         }
-        if (half == 0 && row < a.sq) {
+        if (half == 0 && row < rows) {
             float* lp = sp.lse_part + ((int64_t(split) * bhs + bh) * a.sq + row) * 2;
             const float sb = st.m + __builtin_amdgcn_logf(st.lb);
             lp[0] = sb;

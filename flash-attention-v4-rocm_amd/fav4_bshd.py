@@ -85,6 +85,13 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
         lib.fav4_bshd_splitkv_workspace_size.restype = C.c_longlong
         lib.fav4_bshd_splitkv_select.argtypes = [C.POINTER(Args), C.c_int]
         lib.fav4_bshd_splitkv_select.restype = C.c_int
+        lib.fav4_bshd_forward_splitkv_gqa.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                                      C.c_size_t, C.c_void_p]
+        lib.fav4_bshd_forward_splitkv_gqa.restype = C.c_int
+        lib.fav4_bshd_splitkv_gqa_workspace_size.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_int]
+        lib.fav4_bshd_splitkv_gqa_workspace_size.restype = C.c_longlong
+        lib.fav4_bshd_splitkv_gqa_select.argtypes = [C.POINTER(Args), C.c_int, C.c_int]
+        lib.fav4_bshd_splitkv_gqa_select.restype = C.c_int
         lib.fav4_bshd_forward_gqa.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_int, C.c_void_p]
         lib.fav4_bshd_forward_gqa.restype = C.c_int
         lib.fav4_bshd_forward_strided.argtypes = [C.POINTER(Args), C.c_int] + [C.POINTER(Strides)] * 4 + [
@@ -144,28 +151,44 @@ class Runner:
     def shape_args(batch, heads, sq, sk) -> Args:
         return Args(None, None, None, None, None, batch, heads, sq, sk, 1 / math.sqrt(D))
 
-    def splitkv_select(self, batch, heads, sq, sk, causal) -> int:
-        return self.hip.fav4_bshd_splitkv_select(C.byref(self.shape_args(batch, heads, sq, sk)), int(causal))
-
-    def splitkv_workspace_size(self, batch, heads, sq, sk, causal, splits=0) -> int:
+    def splitkv_select(self, batch, heads, sq, sk, causal, kv_heads=None) -> int:
         a = self.shape_args(batch, heads, sq, sk)
-        return self.hip.fav4_bshd_splitkv_workspace_size(C.byref(a), int(causal), int(splits))
+        if kv_heads is None:
+            return self.hip.fav4_bshd_splitkv_select(C.byref(a), int(causal))
+        return self.hip.fav4_bshd_splitkv_gqa_select(C.byref(a), int(kv_heads), int(causal))
+
+    def splitkv_workspace_size(self, batch, heads, sq, sk, causal, splits=0, kv_heads=None) -> int:
+        a = self.shape_args(batch, heads, sq, sk)
+        if kv_heads is None:
+            return self.hip.fav4_bshd_splitkv_workspace_size(C.byref(a), int(causal), int(splits))
+        return self.hip.fav4_bshd_splitkv_gqa_workspace_size(C.byref(a), int(kv_heads), int(causal), int(splits))
 
     def call_splitkv(self, q, k, v, o, lse, causal, splits=0, workspace=None, scale=None, stream=None):
-        """Split-KV forward.  `workspace` is a CUDA tensor (any dtype, 256-byte aligned);
-        None allocates one of the required size here (the library never allocates)."""
+        """Split-KV forward; K/V heads = k.shape[2] (fewer than q's: the GQA
+        entry point).  `workspace` is a CUDA tensor (any dtype, 256-byte
+        aligned); None allocates one of the required size here (the library
+        never allocates)."""
         import torch
-        a = self.args(q, k, v, o, lse, scale)
+        kvh = k.shape[2]
+        gqa = kvh != q.shape[2]
+        a = self.args(q, k, v, o, lse, scale, kv_heads=kvh)
         if workspace is None:
-            need = self.hip.fav4_bshd_splitkv_workspace_size(C.byref(a), int(causal), int(splits))
+            if gqa:
+                need = self.hip.fav4_bshd_splitkv_gqa_workspace_size(C.byref(a), int(kvh), int(causal), int(splits))
+            else:
+                need = self.hip.fav4_bshd_splitkv_workspace_size(C.byref(a), int(causal), int(splits))
             if need < 0:
                 raise RuntimeError(f"splits {splits}: arguments rejected")
             workspace = torch.empty(max(need, 1), device=q.device, dtype=torch.uint8)
         nbytes = workspace.numel() * workspace.element_size()
         if stream is None:
             stream = torch.cuda.current_stream().cuda_stream
-        status = self.hip.fav4_bshd_forward_splitkv(C.byref(a), int(causal), int(splits), workspace.data_ptr(),
-                                                     nbytes, stream)
+        if gqa:
+            status = self.hip.fav4_bshd_forward_splitkv_gqa(C.byref(a), int(kvh), int(causal), int(splits),
+                                                             workspace.data_ptr(), nbytes, stream)
+        else:
+            status = self.hip.fav4_bshd_forward_splitkv(C.byref(a), int(causal), int(splits), workspace.data_ptr(),
+                                                         nbytes, stream)
         if status:
             raise RuntimeError(f"splitkv splits {splits}: HIP status {status}")
         return workspace

@@ -71,6 +71,22 @@ extern "C" long long fav4_bshd_splitkv_workspace_size(const Fav4Args* args, int 
 // The chunk count that splits = 0 resolves to (1 = no split), or -1.
 extern "C" int fav4_bshd_splitkv_select(const Fav4Args* args, int causal);
 
+// Split-KV with grouped K/V heads (GQA / MQA); no counterpart in the
+// reference.  K and V are [B, Sk, kv_heads, 128] with kv_heads dividing
+// args->heads (query head h reads K/V head h / (heads / kv_heads)), as in
+// fav4_bshd_forward_gqa; otherwise the contract of the split-KV calls above,
+// which are these with kv_heads = heads.  For Sq <= 32 (decode) the query
+// heads that share a K/V head are packed into one 32-row tile (row =
+// head-in-group * Sq + query), so each K/V head is streamed once per group
+// instead of once per query head.  Per row the result is bitwise that of the
+// MHA split-KV call on K/V with their heads repeated group-wise at the same
+// explicit chunk count.  Splits resolving to 1 run fav4_bshd_forward_gqa.
+extern "C" int fav4_bshd_forward_splitkv_gqa(const Fav4Args* args, int kv_heads, int causal, int splits,
+                                             void* workspace, size_t workspace_bytes, hipStream_t stream);
+extern "C" long long fav4_bshd_splitkv_gqa_workspace_size(const Fav4Args* args, int kv_heads, int causal,
+                                                          int splits);
+extern "C" int fav4_bshd_splitkv_gqa_select(const Fav4Args* args, int kv_heads, int causal);
+
 // ---- Grouped-query / multi-query attention ----------------------------------
 // No counterpart in the reference (its README lists GQA as unsupported).  The
 // same contract as fav4_bshd_forward, except that K and V are

@@ -47,7 +47,8 @@ def test_exports_exactly_the_c_abi():
     public = {n for n in names if not n.startswith("_")}
     assert public == {"fav4_bshd_forward", "fav4_bshd_select_config", "fav4_bshd_forward_splitkv",
                       "fav4_bshd_splitkv_workspace_size", "fav4_bshd_splitkv_select", "fav4_bshd_forward_gqa",
-                      "fav4_bshd_forward_varlen", "fav4_bshd_forward_strided"}, public
+                      "fav4_bshd_forward_varlen", "fav4_bshd_forward_strided", "fav4_bshd_forward_splitkv_gqa",
+                      "fav4_bshd_splitkv_gqa_workspace_size", "fav4_bshd_splitkv_gqa_select"}, public
 
 
 def test_ctypes_layout_matches_reference(Args):
@@ -141,17 +142,19 @@ def test_runner_rejects_host_tensors():
 
 # ---- split-KV queries -------------------------------------------------------
 
-def _split_plan(b, h, sq, sk, splits, cus=None, causal=False):
+def _split_plan(b, h, sq, sk, splits, cus=None, causal=False, kvh=None):
     """Closed form of the split plan: key tiles over the keys a row can see
-    (min(sk, sq) for top-left causal); 256-row q tiles and 64-key tiles, one
-    workgroup per CU and at most 64 Auto chunks -- or, for sq <= 32 (decode),
-    32-row q tiles, 32-key tiles, three workgroups per CU and at most 128;
-    splits=0 picks ceil(CUs * per_cu / items) capped by min(max, ktiles // 4);
-    then tiles-per-chunk and the final count so that no chunk is empty."""
+    (min(sk, sq) for top-left causal); 256-row q tiles of one head and 64-key
+    tiles, one workgroup per CU and at most 64 Auto chunks -- or, for sq <= 32
+    (decode), 32-row tiles of a K/V head's packed (h / kvh) * sq query rows,
+    32-key tiles, three workgroups per CU and at most 128; splits=0 picks
+    ceil(CUs * per_cu / items) capped by min(max, ktiles // 4); then
+    tiles-per-chunk and the final count so that no chunk is empty."""
+    kvh = h if kvh is None else kvh
     bm, bn, per_cu, amax = (32, 32, 3, 128) if sq <= 32 else (256, 64, 1, 64)
     ktiles = -(-(min(sk, sq) if causal else sk) // bn)
     if splits == 0:
-        items = b * h * -(-sq // bm)
+        items = b * kvh * -(-(h // kvh) * sq // bm) if sq <= 32 else b * h * -(-sq // bm)
         splits = min(-(-(cus * per_cu) // items), min(amax, max(1, ktiles // 4)))
     splits = max(1, min(splits, ktiles))
     tps = -(-ktiles // splits)
@@ -197,6 +200,31 @@ def test_splitkv_plan_examples():
     assert _split_plan(1, 1, 256, 65536, 0, cus=256) == (64, 16)
     # causal B1 H8 Sq1024 Sk32768 sees only the first 1024 keys: 4 chunks of 4 tiles
     assert _split_plan(1, 8, 1024, 32768, 0, cus=256, causal=True) == (4, 4)
+    # GQA decode B4 H32 KVH8 Sq1 Sk32768: 4 heads of a group share one 32-row
+    # tile, 32 items, 1024 key tiles -> 24 chunks of 43
+    assert _split_plan(4, 32, 1, 32768, 0, cus=256, kvh=8) == (24, 43)
+    # MQA decode, 16 queries x 8 heads = 128 packed rows = 4 tiles per batch:
+    # 96 chunks wanted over 512 key tiles -> 86 of 6
+    assert _split_plan(2, 8, 16, 16384, 0, cus=256, kvh=1) == (86, 6)
+
+
+@pytest.mark.parametrize("shape", [(4, 32, 8, 1, 32768), (2, 8, 1, 16, 16384), (1, 12, 3, 5, 4000),
+                                   (3, 6, 2, 100, 9000), (1, 8, 8, 1, 65536)])
+def test_splitkv_gqa_plan(lib, Args, shape):
+    """GQA split plan (decode packs a group's query heads into shared tiles)
+    and its workspace, plus the rejected K/V head counts."""
+    b, h, kvh, sq, sk = shape
+    a = Args(None, None, None, None, None, b, h, sq, sk, 1 / math.sqrt(128))
+    for causal in (0, 1):
+        n, _ = _split_plan(b, h, sq, sk, 0, cus=256, causal=bool(causal), kvh=kvh)
+        assert lib.fav4_bshd_splitkv_gqa_select(C.byref(a), kvh, causal) == n
+        want = 0 if n == 1 else n * b * h * sq * (128 * 4 + 8)
+        assert lib.fav4_bshd_splitkv_gqa_workspace_size(C.byref(a), kvh, causal, 0) == want
+        for bad in (0, -1, h + 1, 5 if h % 5 else 7):
+            if bad > 0 and h % bad == 0:
+                continue
+            assert lib.fav4_bshd_splitkv_gqa_select(C.byref(a), bad, causal) == -1
+            assert lib.fav4_bshd_splitkv_gqa_workspace_size(C.byref(a), bad, causal, 0) == -1
 
 
 @pytest.mark.parametrize("causal,splits,sq", [(2, 4, 256), (-1, 4, 256), (0, -1, 256), (0, 257, 256),

@@ -24,7 +24,9 @@ def _run(gpu_runner, torch, q, k, v, causal, splits, with_lse, ws_fill=None):
     b, sq, h, _ = q.shape
     o = torch.full_like(qd, float("nan"))
     lse = torch.full((b, h, sq), float("nan"), device=dev, dtype=torch.float32) if with_lse else None
-    need = gpu_runner.splitkv_workspace_size(b, h, sq, k.shape[1], causal, splits)
+    kvh = k.shape[2]
+    need = gpu_runner.splitkv_workspace_size(b, h, sq, k.shape[1], causal, splits,
+                                             kv_heads=None if kvh == h else kvh)
     assert need >= 0
     ws = torch.empty(max(need, 1), device=dev, dtype=torch.uint8)
     if ws_fill is not None and need >= 4:
@@ -157,3 +159,33 @@ def test_splitkv_many_chunks(gpu_runner, case):
             o, lse = _run(gpu_runner, torch, q, k, v, causal, splits, with_lse)
             e = orc.errors(o, lse, ref, ref_lse if with_lse else None)
             assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (splits, with_lse, e)
+
+
+GQA = [(2, 8, 2, 1, 5000), (1, 12, 3, 5, 4000), (3, 6, 2, 20, 1500), (2, 8, 1, 16, 3000), (1, 8, 4, 100, 2000),
+       (1, 32, 8, 1, 40000)]
+
+
+@pytest.mark.parametrize("shape", GQA, ids=lambda s: "b%dh%dkv%d_%dx%d" % s)
+def test_splitkv_gqa(gpu_runner, shape):
+    """fav4_bshd_forward_splitkv_gqa: decode shapes (Sq <= 32) pack the query
+    heads of a K/V head into shared 32-row tiles, longer ones run one head per
+    item.  Against the FP64 oracle (Auto and explicit chunks), and at an
+    explicit chunk count bitwise equal to the MHA split-KV call on K/V with
+    their heads repeated group-wise (per row, the packed tile computes exactly
+    what a tile of that head alone does)."""
+    import torch
+    b, h, kvh, sq, sk = shape
+    group = h // kvh
+    q, _, _ = orc.make_inputs(b, h, sq, sk, "normal", seed=41)
+    _, k, v = orc.make_inputs(b, kvh, sq, sk, "normal", seed=42)
+    ke, ve = np.repeat(k, group, axis=2), np.repeat(v, group, axis=2)
+    for causal in (False, True):
+        ref, ref_lse = orc.attention_fp64(q, ke, ve, orc.DEFAULT_SCALE, causal)
+        for splits in (0, 3):
+            o, lse = _run(gpu_runner, torch, q, k, v, causal, splits, True)
+            e = orc.errors(o, lse, ref, ref_lse)
+            assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (causal, splits, e)
+            if splits:
+                om, lsem = _run(gpu_runner, torch, q, ke, ve, causal, splits, True)
+                assert np.array_equal(o, om), (causal, "O differs from MHA on repeated heads")
+                assert np.array_equal(lse.view(np.int32), lsem.view(np.int32)), (causal, "LSE differs")
