@@ -81,6 +81,21 @@ def test_graph_splitkv(gpu_runner, causal):
     _check_graph(torch, lambda: gpu_runner.call_splitkv(q, k, v, o, lse, causal, 6, workspace=ws), [o, lse], noise)
 
 
+def test_graph_splitkv_gqa_decode(gpu_runner):
+    """The packed GQA decode (one-wave partial kernel + grouped merge)."""
+    import torch
+    q, _, _ = _inputs(torch, 2, 16, 3, 5000)
+    _, k, v = _inputs(torch, 2, 16, 3, 5000, kvh=4, seed=7)
+    o = torch.empty_like(q)
+    lse = torch.empty((2, 16, 3), device="cuda", dtype=torch.float32)
+    need = gpu_runner.splitkv_workspace_size(2, 16, 3, 5000, False, 40, kv_heads=4)
+    ws = torch.empty(max(need, 256), device="cuda", dtype=torch.uint8)
+    on = torch.empty_like(q)
+    noise = lambda: gpu_runner.call_splitkv(q, k, v, on, None, False, 9, workspace=ws)
+    print("  graph splitkv gqa decode", flush=True)
+    _check_graph(torch, lambda: gpu_runner.call_splitkv(q, k, v, o, lse, False, 40, workspace=ws), [o, lse], noise)
+
+
 @pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
 def test_graph_varlen_and_strided(gpu_runner, causal):
     import torch
