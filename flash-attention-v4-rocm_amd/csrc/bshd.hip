@@ -157,6 +157,10 @@ int split_shape_ok(const Fav4Args* a, int kv_heads, int causal, int splits) {
         a->sk > INT_MAX / (a->heads * 128) || splits < 0 || splits > fav4::MAX_SPLITS || a->sq > MAX_SPLIT_SQ ||
         kv_heads <= 0 || kv_heads > a->heads || a->heads % kv_heads != 0)
         return hipErrorInvalidValue;
+    // Decode packs a group's (heads / kv_heads) * sq rows into one row space,
+    // whose FP32 partial rows must fit a 4 GiB buffer bound.
+    if (a->sq <= DECODE_SQ && int64_t(a->heads / kv_heads) * a->sq * fav4::D * 4 > int64_t(UINT32_MAX))
+        return hipErrorInvalidValue;
     return hipSuccess;
 }
 

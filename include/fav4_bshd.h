@@ -81,6 +81,8 @@ extern "C" int fav4_bshd_splitkv_select(const Fav4Args* args, int causal);
 // instead of once per query head.  Per row the result is bitwise that of the
 // MHA split-KV call on K/V with their heads repeated group-wise at the same
 // explicit chunk count.  Splits resolving to 1 run fav4_bshd_forward_gqa.
+// For Sq <= 32, (heads / kv_heads) * Sq must stay below 2^23 (one group's
+// partial rows within a 4 GiB buffer bound).
 extern "C" int fav4_bshd_forward_splitkv_gqa(const Fav4Args* args, int kv_heads, int causal, int splits,
                                              void* workspace, size_t workspace_bytes, hipStream_t stream);
 extern "C" long long fav4_bshd_splitkv_gqa_workspace_size(const Fav4Args* args, int kv_heads, int causal,

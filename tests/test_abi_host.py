@@ -227,6 +227,15 @@ def test_splitkv_gqa_plan(lib, Args, shape):
             assert lib.fav4_bshd_splitkv_gqa_workspace_size(C.byref(a), bad, causal, 0) == -1
 
 
+def test_splitkv_gqa_rejects_oversized_groups(lib, Args):
+    """Decode packs (heads / kv_heads) * sq rows of 512 partial bytes into one
+    4 GiB-bounded buffer: 2^23 rows is one too many."""
+    a = Args(None, None, None, None, None, 1, 1 << 18, 32, 64, 1 / math.sqrt(128))
+    assert lib.fav4_bshd_splitkv_gqa_select(C.byref(a), 1, 0) == -1
+    a.heads = (1 << 18) - 8
+    assert lib.fav4_bshd_splitkv_gqa_select(C.byref(a), 1, 0) >= 1
+
+
 @pytest.mark.parametrize("causal,splits,sq", [(2, 4, 256), (-1, 4, 256), (0, -1, 256), (0, 257, 256),
                                               (0, 4, (1 << 22) + 1)])
 def test_splitkv_queries_reject(lib, Args, causal, splits, sq):
