@@ -406,6 +406,49 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
                          "splits": splits, "us": round(us, 2), "kv_tbps": round(kv_bytes / us / 1e6, 2)}
     del q, k, v, o, ws
     torch.cuda.empty_cache()
+
+    # Continuous-batching decode: packed sequences, one new query each, ragged
+    # cache lengths; split-KV over the packed batch against the unsplit packed
+    # forward.  Reported as K+V bandwidth.
+    vb, vh, vkvh = 32, 32, 8
+    klens = np.random.default_rng(4242).integers(1024, 32768 + 1, size=vb)
+    cuk_h = np.concatenate([[0], np.cumsum(klens)]).astype(np.int32)
+    cuq_h = np.arange(vb + 1, dtype=np.int32)
+    tk, mk_len = int(cuk_h[-1]), int(klens.max())
+    cuq, cuk = torch.from_numpy(cuq_h).cuda(), torch.from_numpy(cuk_h).cuda()
+    q, k, v = mk(vb, vh, 128), mk(tk, vkvh, 128), mk(tk, vkvh, 128)
+    o = torch.empty_like(q)
+    need = runner.splitkv_varlen_workspace_size(vb, vh, vkvh, 1, mk_len, vb, tk, False)
+    ws = torch.empty(max(need, 256), device="cuda", dtype=torch.uint8)
+    splits = runner.splitkv_varlen_select(vb, vh, vkvh, 1, mk_len, vb, tk, False)
+    kv_bytes = 2 * tk * vkvh * 256
+    grp = vh // vkvh
+    res = {"workload": f"{vb} sequences x 1 query, cache lengths {int(klens.min())}..{mk_len} (seeded), {tk} keys, "
+                       f"H{vh} KV heads {vkvh} D128 BF16 dense", "splits": splits}
+    fns = (("plain", lambda: runner.call_varlen(q, k, v, o, None, cuq, cuk, 1, mk_len, False,
+                                                stream=stream.cuda_stream)),
+           ("splitkv", lambda: runner.call_splitkv_varlen(q, k, v, o, None, cuq, cuk, 1, mk_len, False, 0,
+                                                          workspace=ws, stream=stream.cuda_stream)))
+    for name, fn in fns:
+        o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            fn()
+        torch.cuda.synchronize()
+        for i in (0, int(np.argmax(klens))):
+            ks, ke = int(cuk_h[i]), int(cuk_h[i + 1])
+            err, _ = check_rows(torch, orc, q[i:i + 1][None], k[ks:ke][None].repeat_interleave(grp, dim=2),
+                                v[ks:ke][None].repeat_interleave(grp, dim=2), o[i:i + 1][None], False,
+                                [(0, 0), (0, vh - 1)])
+            if not orc.check_acceptance_tolerance(err):
+                raise SystemExit(f"api report: varlen decode {name} check failed: {err}")
+        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+        res[name] = {"us": round(us, 2), "kv_tbps": round(kv_bytes / us / 1e6, 2)}
+        print(f"# varlen decode {name}: {us:.1f} us, K+V {kv_bytes / us / 1e6:.2f} TB/s", file=sys.stderr, flush=True)
+    res["speedup"] = round(res["plain"]["us"] / res["splitkv"]["us"], 2)
+    out["varlen_decode"] = res
+    del q, k, v, o, ws
+    torch.cuda.empty_cache()
     return out
 
 

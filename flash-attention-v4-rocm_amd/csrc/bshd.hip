@@ -169,41 +169,50 @@ int split_args_ok(const Fav4Args* a, int kv_heads, int causal, int splits) {
     return st != hipSuccess ? st : split_shape_ok(a, kv_heads, causal, splits);
 }
 
-template <bool CAUSAL>
-int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, hipStream_t stream) {
+// VARLEN: `a` holds the packed batch's shape (max lengths) and `sp` its
+// sequence offsets; decode shape only.  Top-left causal decode (sq <= 32) sees
+// at most 32 keys, one tile, so the plan never splits it: causal launches use
+// the prefill shape only.
+template <bool CAUSAL, bool VARLEN = false>
+int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, fav4::SplitArgs sp,
+                 hipStream_t stream) {
+    static_assert(!(CAUSAL && VARLEN), "causal decode never splits");
     const int tiles = p.tiles;
     const int64_t total = p.items * tiles * p.splits;
     const int64_t rows = int64_t(a.batch) * a.heads * a.sq;
-    if (total > INT_MAX || rows > INT_MAX) return hipErrorInvalidValue;
-    fav4::SplitArgs sp;
+    const bool decode = p.shape.bm == 32;
+    if (total > INT_MAX || rows > INT_MAX || (VARLEN && !decode) || (CAUSAL && decode)) return hipErrorInvalidValue;
     sp.o_part = static_cast<float*>(ws);
     sp.lse_part = sp.o_part + int64_t(p.splits) * rows * fav4::D;
     sp.splits = p.splits;
     sp.tps = p.tps;
     const int grid = int(total < MAX_GRID ? total : MAX_GRID);
     // The FP32 sums only feed an LSE output.
-    if (p.shape.bm == 32 && a.lse)
-        hipLaunchKernelGGL((fav4::fwd_kernel_split<32, CAUSAL, 1, true>), dim3(grid), dim3(64), 0, stream, a, sp,
-                           kv_heads, tiles, int(total));
-    else if (p.shape.bm == 32)
-        hipLaunchKernelGGL((fav4::fwd_kernel_split<32, CAUSAL, 1, false>), dim3(grid), dim3(64), 0, stream, a, sp,
-                           kv_heads, tiles, int(total));
-    else if (a.lse)
-        hipLaunchKernelGGL((fav4::fwd_kernel_split<64, CAUSAL, 8, true>), dim3(grid), dim3(512), 0, stream, a, sp,
-                           kv_heads, tiles, int(total));
-    else
-        hipLaunchKernelGGL((fav4::fwd_kernel_split<64, CAUSAL, 8, false>), dim3(grid), dim3(512), 0, stream, a, sp,
-                           kv_heads, tiles, int(total));
+    auto go = [&](auto kernel, int threads) {
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, stream, a, sp, kv_heads, tiles, int(total));
+    };
+    if constexpr (VARLEN) {
+        if (a.lse) go(fav4::fwd_kernel_split<32, false, 1, true, true>, 64);
+        else go(fav4::fwd_kernel_split<32, false, 1, false, true>, 64);
+    } else if constexpr (CAUSAL) {
+        if (a.lse) go(fav4::fwd_kernel_split<64, true, 8, true>, 512);
+        else go(fav4::fwd_kernel_split<64, true, 8, false>, 512);
+    } else {
+        if (decode && a.lse) go(fav4::fwd_kernel_split<32, false, 1, true>, 64);
+        else if (decode) go(fav4::fwd_kernel_split<32, false, 1, false>, 64);
+        else if (a.lse) go(fav4::fwd_kernel_split<64, false, 8, true>, 512);
+        else go(fav4::fwd_kernel_split<64, false, 8, false>, 512);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // Lane groups per merged row: one per 8 chunks, at most 8 (one workgroup).
     const int per = p.splits <= 8 ? 1 : p.splits <= 16 ? 2 : p.splits <= 32 ? 4 : 8;
     const int64_t row_blocks = (rows * per + 7) / 8;
     const unsigned blocks = unsigned(row_blocks < MAX_GRID ? row_blocks : MAX_GRID);
-    if (per == 1) hipLaunchKernelGGL(fav4::combine_kernel<1>, dim3(blocks), dim3(256), 0, stream, a, sp);
-    else if (per == 2) hipLaunchKernelGGL(fav4::combine_kernel<2>, dim3(blocks), dim3(256), 0, stream, a, sp);
-    else if (per == 4) hipLaunchKernelGGL(fav4::combine_kernel<4>, dim3(blocks), dim3(256), 0, stream, a, sp);
-    else hipLaunchKernelGGL(fav4::combine_kernel<8>, dim3(blocks), dim3(256), 0, stream, a, sp);
+    if (per == 1) hipLaunchKernelGGL((fav4::combine_kernel<1, VARLEN>), dim3(blocks), dim3(256), 0, stream, a, sp);
+    else if (per == 2) hipLaunchKernelGGL((fav4::combine_kernel<2, VARLEN>), dim3(blocks), dim3(256), 0, stream, a, sp);
+    else if (per == 4) hipLaunchKernelGGL((fav4::combine_kernel<4, VARLEN>), dim3(blocks), dim3(256), 0, stream, a, sp);
+    else hipLaunchKernelGGL((fav4::combine_kernel<8, VARLEN>), dim3(blocks), dim3(256), 0, stream, a, sp);
     return hipGetLastError();
 }
 
@@ -218,6 +227,73 @@ void launch_varlen(const Fav4VarlenArgs& a, int causal, int tiles, int total, in
         hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, false, true, WAVES>), dim3(grid), block, 0, stream, a, tiles, total);
     else
         hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, false, false, WAVES>), dim3(grid), block, 0, stream, a, tiles, total);
+}
+
+// Checks of the packed-sequence arguments (before any HIP call); the shape
+// checks alone serve the queries that take no buffers.
+int varlen_shape_ok(const Fav4VarlenArgs* a, int causal) {
+    if (!a || a->batch <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads != 0 ||
+        a->max_seqlen_q <= 0 || a->max_seqlen_k <= 0 || a->total_q <= 0 || a->total_k <= 0 ||
+        (causal != 0 && causal != 1) || !std::isfinite(a->scale) || a->scale <= 0)
+        return hipErrorInvalidValue;
+    if (a->batch > INT_MAX - 1 || a->heads > INT_MAX / 256 ||
+        int64_t(a->max_seqlen_q) * a->heads * 256 > int64_t(UINT32_MAX) ||
+        int64_t(a->max_seqlen_k) * a->kv_heads * 256 > int64_t(UINT32_MAX))
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+int varlen_ok(const Fav4VarlenArgs* a, int causal) {
+    if (varlen_shape_ok(a, causal) != hipSuccess || !a->q || !a->k || !a->v || !a->o || !a->cu_seqlens_q ||
+        !a->cu_seqlens_k ||
+        ((reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->k) |
+          reinterpret_cast<uintptr_t>(a->v) | reinterpret_cast<uintptr_t>(a->o)) & 15) ||
+        ((reinterpret_cast<uintptr_t>(a->cu_seqlens_q) | reinterpret_cast<uintptr_t>(a->cu_seqlens_k)) & 3) ||
+        (a->lse && (reinterpret_cast<uintptr_t>(a->lse) & 3)))
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+// The packed batch as the split-KV kernels see it: sq / sk are the longest
+// sequence's lengths, LSE is [heads, total_q].
+Fav4Args varlen_shape(const Fav4VarlenArgs& v) {
+    Fav4Args a{};
+    a.q = v.q; a.k = v.k; a.v = v.v; a.o = v.o; a.lse = v.lse;
+    a.batch = v.batch; a.heads = v.heads; a.sq = v.max_seqlen_q; a.sk = v.max_seqlen_k;
+    a.scale = v.scale;
+    return a;
+}
+
+// Split-KV of packed decode batches (max_seqlen_q <= 32; longer queries take
+// one chunk, the plain packed forward).  Chunks are a fixed number of key
+// tiles for every sequence, so a sequence has as many non-empty chunks as its
+// keys need.  Auto takes the chunk size of the contiguous-batch Auto plan at
+// the mean key length (total_k / batch), enlarged if the longest sequence
+// would need more than MAX_SPLITS chunks: a ragged batch's long sequences
+// thus spread over as many workgroups as a uniform batch's, and a uniform
+// batch gets exactly the contiguous plan.
+SplitPlan varlen_split_plan(const Fav4VarlenArgs& v, int causal, int req) {
+    const Fav4Args a = varlen_shape(v);
+    if (a.sq > DECODE_SQ) return {1, 1, split_shape(a), 1, 1};
+    SplitPlan p = split_plan(a, v.kv_heads, causal, req == 0 ? 1 : req);
+    if (req == 0) {
+        Fav4Args mean = a;
+        mean.sk = int(std::max<int64_t>(1, std::min<int64_t>(a.sk, (int64_t(v.total_k) + v.batch - 1) / v.batch)));
+        const int keys = causal ? std::min(a.sk, a.sq) : a.sk;
+        const int ktiles = (keys + p.shape.bn - 1) / p.shape.bn;
+        p.tps = std::max(split_plan(mean, v.kv_heads, causal, 0).tps, (ktiles + fav4::MAX_SPLITS - 1) / fav4::MAX_SPLITS);
+        p.splits = (ktiles + p.tps - 1) / p.tps;
+    }
+    return p;
+}
+
+int varlen_split_ok(const Fav4VarlenArgs* v, int causal, int splits, bool buffers) {
+    const int st = buffers ? varlen_ok(v, causal) : varlen_shape_ok(v, causal);
+    if (st != hipSuccess) return st;
+    if (splits < 0 || splits > fav4::MAX_SPLITS) return hipErrorInvalidValue;
+    if (v->max_seqlen_q > DECODE_SQ) return hipSuccess;
+    const Fav4Args a = varlen_shape(*v);
+    return split_shape_ok(&a, v->kv_heads, causal, splits);
 }
 
 // Auto: 128-row workgroups (config 1; two per CU, so one's prologue and
@@ -281,19 +357,8 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_strided(
 // Packed variable-length sequences (no counterpart in the reference).
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_varlen(const Fav4VarlenArgs* a, int causal,
                                                                        hipStream_t stream) {
-    if (!a || !a->q || !a->k || !a->v || !a->o || !a->cu_seqlens_q || !a->cu_seqlens_k || a->batch <= 0 ||
-        a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads != 0 || a->max_seqlen_q <= 0 ||
-        a->max_seqlen_k <= 0 || a->total_q <= 0 || a->total_k <= 0 || (causal != 0 && causal != 1) ||
-        !std::isfinite(a->scale) || a->scale <= 0)
-        return hipErrorInvalidValue;
-    if (a->batch > INT_MAX - 1 || a->heads > INT_MAX / 256 ||
-        int64_t(a->max_seqlen_q) * a->heads * 256 > int64_t(UINT32_MAX) ||
-        int64_t(a->max_seqlen_k) * a->kv_heads * 256 > int64_t(UINT32_MAX) ||
-        ((reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->k) |
-          reinterpret_cast<uintptr_t>(a->v) | reinterpret_cast<uintptr_t>(a->o)) & 15) ||
-        ((reinterpret_cast<uintptr_t>(a->cu_seqlens_q) | reinterpret_cast<uintptr_t>(a->cu_seqlens_k)) & 3) ||
-        (a->lse && (reinterpret_cast<uintptr_t>(a->lse) & 3)))
-        return hipErrorInvalidValue;
+    const int st = varlen_ok(a, causal);
+    if (st != hipSuccess) return st;
     // The forward's Auto rule on the longest sequence: 128-row tiles (4 waves)
     // for max_seqlen_q <= 1024 or when 256-row tiles would give fewer
     // (sequence, head, q tile) items than CUs; else 256-row tiles.
@@ -350,8 +415,9 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_
     const int64_t need = split_workspace(*a, p);
     if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || uint64_t(need) > workspace_bytes)
         return hipErrorInvalidValue;
-    return causal ? launch_split<true>(*a, kv_heads, p, workspace, stream)
-                  : launch_split<false>(*a, kv_heads, p, workspace, stream);
+    const fav4::SplitArgs sp{};
+    return causal ? launch_split<true>(*a, kv_heads, p, workspace, sp, stream)
+                  : launch_split<false>(*a, kv_heads, p, workspace, sp, stream);
 }
 
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_splitkv_select(const Fav4Args* a, int causal) {
@@ -369,4 +435,40 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv(
                                                                         hipStream_t stream) {
     if (!a) return hipErrorInvalidValue;
     return fav4_bshd_forward_splitkv_gqa(a, a->heads, causal, splits, workspace, workspace_bytes, stream);
+}
+
+// Split-KV of packed variable-length batches (no counterpart in the reference).
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_splitkv_varlen_select(const Fav4VarlenArgs* a,
+                                                                              int causal) {
+    if (varlen_split_ok(a, causal, 0, false) != hipSuccess) return -1;
+    return varlen_split_plan(*a, causal, 0).splits;
+}
+
+extern "C" __attribute__((visibility("default"))) long long fav4_bshd_splitkv_varlen_workspace_size(
+    const Fav4VarlenArgs* a, int causal, int splits) {
+    if (varlen_split_ok(a, causal, splits, false) != hipSuccess) return -1;
+    return split_workspace(varlen_shape(*a), varlen_split_plan(*a, causal, splits));
+}
+
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_varlen(const Fav4VarlenArgs* a,
+                                                                               int causal, int splits,
+                                                                               void* workspace,
+                                                                               size_t workspace_bytes,
+                                                                               hipStream_t stream) {
+    const int st = varlen_split_ok(a, causal, splits, true);
+    if (st != hipSuccess) return st;
+    const SplitPlan p = varlen_split_plan(*a, causal, splits);
+    // Top-left causal decode (max_seqlen_q <= 32) sees at most 32 keys, one
+    // tile: the plan never splits it.
+    if (p.splits == 1 || causal) return fav4_bshd_forward_varlen(a, causal, stream);
+    const Fav4Args shape = varlen_shape(*a);
+    const int64_t need = split_workspace(shape, p);
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || uint64_t(need) > workspace_bytes)
+        return hipErrorInvalidValue;
+    fav4::SplitArgs sp{};
+    sp.cu_q = a->cu_seqlens_q;
+    sp.cu_k = a->cu_seqlens_k;
+    sp.total_q = a->total_q;
+    sp.total_k = a->total_k;
+    return launch_split<false, true>(shape, a->kv_heads, p, workspace, sp, stream);
 }

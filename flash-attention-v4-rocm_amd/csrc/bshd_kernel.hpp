@@ -577,7 +577,31 @@ struct SplitArgs {
     float* o_part;
     float* lse_part;
     int splits, tps;
+    // Packed variable-length sequences (null cu_q: BSHD).  Sequence b's
+    // queries are tokens [cu_q[b], cu_q[b+1]) of Q/O, its keys tokens
+    // [cu_k[b], cu_k[b+1]) of K/V; the Fav4Args shape then carries the
+    // sequence count and max_seqlen_q / max_seqlen_k.
+    const int* cu_q;
+    const int* cu_k;
+    int total_q, total_k;
 };
+
+// Query / key count and first token of sequence b, read on the device and
+// clamped to [0, total] and to the max lengths, as fwd_kernel_varlen does.
+// UNIFORM: b is the same in every lane (the offsets then live in SGPRs).
+struct SeqSpan {
+    int sq, sk;
+    int64_t qtok, ktok;
+};
+template <bool UNIFORM>
+__device__ __forceinline__ SeqSpan seq_span(const SplitArgs& sp, int b, int max_q, int max_k) {
+    auto rd = [](int x) { return UNIFORM ? __builtin_amdgcn_readfirstlane(x) : x; };
+    const int qs = min(max(rd(sp.cu_q[b]), 0), sp.total_q);
+    const int qe = min(max(rd(sp.cu_q[b + 1]), qs), min(sp.total_q, qs + max_q));
+    const int ks = min(max(rd(sp.cu_k[b]), 0), sp.total_k);
+    const int ke = min(max(rd(sp.cu_k[b + 1]), ks), min(sp.total_k, ks + max_k));
+    return {qe - qs, ke - ks, qs, ks};
+}
 
 // Three LDS stages keep two key tiles in flight per workgroup (prefetch
 // distance 2).  Long-key prefill chunks run as fast as with two; decode-like
@@ -588,9 +612,13 @@ struct SplitArgs {
 // three workgroups share a CU and every resident wave computes.
 // LSE: keep the FP32 sums for the LSE output; without it the second log-sum
 // repeats the first (the merge reads it only when writing an LSE).
-template <int BN, bool CAUSAL, int WAVES, bool LSE>
+// VARLEN: packed sequences (one wave only); a.sq / a.sk are the max lengths,
+// packed rows keep the a.sq stride, and rows past a sequence's own length are
+// computed on a valid query but never read by the merge.
+template <int BN, bool CAUSAL, int WAVES, bool LSE, bool VARLEN = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int total) {
+    static_assert(!VARLEN || WAVES == 1, "packed sequences use the one-wave shape");
     constexpr int BM = WAVES * 32, STAGES = 3;
     // One wave (decode): the q-tile rows are the group's query heads times
     // their sq queries, row r = (head - first head of the group) * sq + query,
@@ -655,16 +683,24 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
         const int bh = batch * a.heads + head0;
         const int q0 = tile * BM, qw = q0 + wave * 32;
         const int row = qw + col;                              // row of the item's row space
+        // The sequence: its query / key counts and first tokens.
+        SeqSpan span{a.sq, a.sk, int64_t(batch) * a.sq, int64_t(batch) * a.sk};
+        if constexpr (VARLEN) {
+            span = seq_span<true>(sp, batch, a.sq, a.sk);
+            if (span.sq == 0) continue;                        // no query rows: nothing to merge
+        }
+        const int sq = span.sq, sk = span.sk;
         // This lane's query position (causal limit) and Q byte offset inside
-        // the batch's [sq, heads] block; rows past the space read a valid row.
+        // the sequence's [sq, heads] block; rows past the space (or past the
+        // sequence's queries) read a valid row.
         const int prow = min(row, rows - 1);
         const int qi = PACK ? prow % a.sq : prow;
         const int qhead = PACK ? head0 + prow / a.sq : head0;
-        const int64_t krow0 = int64_t(batch) * a.sk * kv_heads + head0 / group;
+        const int qload = min(qi, sq - 1);
+        const int64_t krow0 = span.ktok * kv_heads + head0 / group;
         const char* kbase = static_cast<const char*>(a.k) + krow0 * ROW_BYTES;
         const char* vbase = static_cast<const char*>(a.v) + krow0 * ROW_BYTES;
-        const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + int64_t(batch) * a.sq * row_bytes,
-                                    uint32_t(a.sq) * row_bytes);
+        const rsrc_t rq = make_rsrc(static_cast<const char*>(a.q) + span.qtok * row_bytes, uint32_t(sq) * row_bytes);
         // This chunk's rows of o_part: [rows - q0][128] FP32 from row q0 (a
         // group's heads are adjacent, so its rows are contiguous).
         const int64_t prow0 = (int64_t(split) * bhs + bh) * a.sq + q0;
@@ -672,9 +708,9 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
         // PACK: every q tile holds rows of query 0 and of the last query, so
         // the causal range is the whole [0, min(sk, sq)) and no tile is
         // unmasked for every row.
-        const int kend = CAUSAL ? min(a.sk, PACK ? a.sq : q0 + BM) : a.sk;
+        const int kend = CAUSAL ? min(sk, PACK ? sq : q0 + BM) : sk;
         const int ntiles = (kend + BN - 1) / BN;
-        const int nfull = (CAUSAL ? (PACK ? 0 : min(a.sk, q0 + 1)) : a.sk) / BN;
+        const int nfull = (CAUSAL ? (PACK ? 0 : min(sk, q0 + 1)) : sk) / BN;
         const int t0 = split * sp.tps, t1 = min(ntiles, t0 + sp.tps);
 
         RowState st;
@@ -690,7 +726,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
             // step reads), keeping the vmcnt count uniform.
             auto issue = [&](int t) {
                 const int64_t first = int64_t(min(t, t1 - 1)) * BN;
-                const uint32_t bytes = uint32_t(a.sk - int(first) - 1) * kv_row_bytes + ROW_BYTES;
+                const uint32_t bytes = uint32_t(sk - int(first) - 1) * kv_row_bytes + ROW_BYTES;
                 const u32x4 rk = make_desc(kbase + first * kv_row_bytes, bytes);
                 const u32x4 rv = make_desc(vbase + first * kv_row_bytes, bytes);
                 const uint32_t ks = smem_base + ((t - t0) % STAGES) * STAGE_BYTES + wave * DMA * 1024;
@@ -704,7 +740,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
             issue(t0 + 1);
             bf16x8 qr[8];
             {
-                const uint32_t qoff = uint32_t(qi) * row_bytes + uint32_t(qhead) * ROW_BYTES + half * 16;
+                const uint32_t qoff = uint32_t(qload) * row_bytes + uint32_t(qhead) * ROW_BYTES + half * 16;
 #pragma unroll
                 for (int c = 0; c < 8; ++c) qr[c] = load16(rq, qoff + c * 32);
 #pragma unroll
@@ -722,7 +758,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
                 const unsigned char* cur = smem + STAGE * STAGE_BYTES;
                 sync_and_prefetch(t);
                 attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE, CAUSAL>(
-                    cur, cur + TILE_BYTES, off, qr, st, t == t0, t * BN, a.sk, qi, half, scale2);
+                    cur, cur + TILE_BYTES, off, qr, st, t == t0, t * BN, sk, qi, half, scale2);
             };
             using S0 = std::integral_constant<int, 0>;
             using S1 = std::integral_constant<int, 1>;
@@ -750,11 +786,13 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
             }
         }
 
-        // Chunk epilogue: FP32 O / lb and the two log2-domain sums.
+        // Chunk epilogue: FP32 O / lb and the two log2-domain sums.  A packed
+        // sequence's chunks past its keys skip the O rows: their log-sums are
+        // -inf, so the merge gives them weight 0 and never adds their O.
         const float inv = st.lb > 0.f ? 1.f / st.lb : 0.f;
         const uint32_t pbase = uint32_t(wave * 32 + col) * (D * 4) + half * 16;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+        for (int db = 0; db < 4 && !(VARLEN && t0 >= t1); ++db) {
 #pragma unroll
             for (int vg = 0; vg < 4; ++vg) {
                 const f32x4 x = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv,
@@ -762,7 +800,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
                 store16(rp, pbase + (db * 32 + vg * 8) * 4, x);
             }
         }
-        if (half == 0 && row < rows) {
+        if (half == 0 && row < rows && qi < sq) {
             float* lp = sp.lse_part + ((int64_t(split) * bhs + bh) * a.sq + row) * 2;
             const float sb = st.m + __builtin_amdgcn_logf(st.lb);
             lp[0] = sb;
@@ -961,6 +999,10 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
 // (4 dims per lane) with no branch between the loads, and the groups' partial
 // sums are added in LDS.  Many chunks over few rows (decode) thus take a few
 // memory round trips instead of one pair of dependent loads per chunk.
+// VARLEN: rows are (sequence, head, query < max_seqlen_q); rows past their
+// sequence's query count are skipped, O goes to the sequence's token rows and
+// LSE to [heads, total_q]; a row whose chunks saw no key gets O = 0 and
+// LSE = -inf.
 constexpr int MAX_SPLITS = 256;
 
 __device__ __forceinline__ float max32(float x) {
@@ -975,7 +1017,7 @@ __device__ __forceinline__ float sum32(float x) {
     return x;
 }
 
-template <int PER>
+template <int PER, bool VARLEN = false>
 __global__ __launch_bounds__(256) void combine_kernel(Fav4Args a, SplitArgs sp) {
     constexpr int RPB = 8 / PER, NT = PER * 32, MAXV = (MAX_SPLITS + NT - 1) / NT;
     __shared__ float wsh[RPB][MAX_SPLITS];   // chunk weights 2^(lse_b,s - max)
@@ -991,7 +1033,18 @@ __global__ __launch_bounds__(256) void combine_kernel(Fav4Args a, SplitArgs sp) 
     // Workgroup-uniform loop: every wave reaches every barrier.
     for (int64_t blk = blockIdx.x; blk < blocks; blk += gridDim.x) {
         const int64_t r = blk * RPB + slot;
-        const bool live = r < rows;
+        const int64_t bh = r / a.sq;
+        const int qi = int(r - bh * a.sq);
+        const int batch = int(bh / a.heads), head = int(bh - int64_t(batch) * a.heads);
+        int64_t qtok = int64_t(batch) * a.sq + qi;       // the row's token (BSHD)
+        bool live = r < rows;
+        if constexpr (VARLEN) {
+            if (live) {
+                const SeqSpan span = seq_span<false>(sp, batch, a.sq, a.sk);
+                live = qi < span.sq;
+                qtok = span.qtok + qi;
+            }
+        }
         float vb[MAXV], vl[MAXV];
         float mb = -__builtin_inff(), ml = -__builtin_inff();
 #pragma unroll
@@ -1014,6 +1067,10 @@ __global__ __launch_bounds__(256) void combine_kernel(Fav4Args a, SplitArgs sp) 
         for (int p = 0; p < PER; ++p) {
             mb = fmaxf(mb, red_m[slot * PER + p].x);
             ml = fmaxf(ml, red_m[slot * PER + p].y);
+        }
+        if constexpr (VARLEN) {
+            // No key in any chunk: weights 2^-inf = 0, so O = 0, LSE = -inf.
+            if (mb == -__builtin_inff()) mb = ml = 0.f;
         }
         float den = 0.f, suml = 0.f;
 #pragma unroll
@@ -1056,16 +1113,18 @@ __global__ __launch_bounds__(256) void combine_kernel(Fav4Args a, SplitArgs sp) 
             for (int p = 1; p < PER; ++p) acc += part_acc[slot * PER + p][q4];
         }
         if (live && part == 0) {
-            const f32x4 y = acc * (1.f / den);
-            const int64_t bh = r / a.sq;
-            const int row = int(r - bh * a.sq);
-            const int batch = int(bh / a.heads), head = int(bh - int64_t(batch) * a.heads);
-            const int64_t orow = (int64_t(batch) * a.sq + row) * a.heads + head;
+            float rden = 1.f / den;
+            if constexpr (VARLEN) rden = den > 0.f ? rden : 0.f;
+            const f32x4 y = acc * rden;
+            const int64_t orow = qtok * a.heads + head;
             const f32x2 y0 = {y[0], y[1]}, y1 = {y[2], y[3]};
             const bf16x2 b0 = __builtin_convertvector(y0, bf16x2), b1 = __builtin_convertvector(y1, bf16x2);
             *reinterpret_cast<bf16x4*>(static_cast<char*>(a.o) + orow * ROW_BYTES + q4 * 8) =
                 bf16x4{b0[0], b0[1], b1[0], b1[1]};
-            if (a.lse && q4 == 0) a.lse[r] = (ml + __builtin_amdgcn_logf(suml)) * LN2;
+            if (a.lse && q4 == 0) {
+                const int64_t li = VARLEN ? int64_t(head) * sp.total_q + qtok : r;
+                a.lse[li] = (ml + __builtin_amdgcn_logf(suml)) * LN2;
+            }
         }
         __syncthreads();   // LDS of this row block is reused by the next
     }

@@ -99,6 +99,13 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
         lib.fav4_bshd_forward_strided.restype = C.c_int
         lib.fav4_bshd_forward_varlen.argtypes = [C.POINTER(VarlenArgs), C.c_int, C.c_void_p]
         lib.fav4_bshd_forward_varlen.restype = C.c_int
+        lib.fav4_bshd_forward_splitkv_varlen.argtypes = [C.POINTER(VarlenArgs), C.c_int, C.c_int, C.c_void_p,
+                                                         C.c_size_t, C.c_void_p]
+        lib.fav4_bshd_forward_splitkv_varlen.restype = C.c_int
+        lib.fav4_bshd_splitkv_varlen_workspace_size.argtypes = [C.POINTER(VarlenArgs), C.c_int, C.c_int]
+        lib.fav4_bshd_splitkv_varlen_workspace_size.restype = C.c_longlong
+        lib.fav4_bshd_splitkv_varlen_select.argtypes = [C.POINTER(VarlenArgs), C.c_int]
+        lib.fav4_bshd_splitkv_varlen_select.restype = C.c_int
         _LIB = lib
     return _LIB
 
@@ -239,6 +246,42 @@ class Runner:
         status = self.hip.fav4_bshd_forward_varlen(C.byref(a), int(causal), stream)
         if status:
             raise RuntimeError(f"varlen: HIP status {status}")
+
+    # ---- split-KV of packed batches (fav4_bshd_forward_splitkv_varlen; no reference counterpart) ----
+    @staticmethod
+    def varlen_shape_args(batch, heads, kv_heads, max_q, max_k, total_q, total_k) -> VarlenArgs:
+        """Shape-only arguments for the select / workspace queries (no buffers)."""
+        return VarlenArgs(None, None, None, None, None, None, None, batch, heads, kv_heads, max_q, max_k,
+                          total_q, total_k, 1 / math.sqrt(D))
+
+    def splitkv_varlen_select(self, batch, heads, kv_heads, max_q, max_k, total_q, total_k, causal) -> int:
+        a = self.varlen_shape_args(batch, heads, kv_heads, max_q, max_k, total_q, total_k)
+        return self.hip.fav4_bshd_splitkv_varlen_select(C.byref(a), int(causal))
+
+    def splitkv_varlen_workspace_size(self, batch, heads, kv_heads, max_q, max_k, total_q, total_k, causal,
+                                      splits=0) -> int:
+        a = self.varlen_shape_args(batch, heads, kv_heads, max_q, max_k, total_q, total_k)
+        return self.hip.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), int(causal), int(splits))
+
+    def call_splitkv_varlen(self, q, k, v, o, lse, cu_q, cu_k, max_q, max_k, causal, splits=0, workspace=None,
+                            scale=None, stream=None):
+        """Split-KV over packed sequences; tensors as for call_varlen.  `workspace`
+        as for call_splitkv (None: allocated here)."""
+        import torch
+        a = self.varlen_args(q, k, v, o, lse, cu_q, cu_k, max_q, max_k, scale)
+        if workspace is None:
+            need = self.hip.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), int(causal), int(splits))
+            if need < 0:
+                raise RuntimeError(f"splitkv varlen splits {splits}: arguments rejected")
+            workspace = torch.empty(max(need, 1), device=q.device, dtype=torch.uint8)
+        nbytes = workspace.numel() * workspace.element_size()
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
+        status = self.hip.fav4_bshd_forward_splitkv_varlen(C.byref(a), int(causal), int(splits),
+                                                            workspace.data_ptr(), nbytes, stream)
+        if status:
+            raise RuntimeError(f"splitkv varlen splits {splits}: HIP status {status}")
+        return workspace
 
 
 def forward(q, k, v, causal=False, with_lse=False, config=0, scale=None):

@@ -127,6 +127,33 @@ struct Fav4VarlenArgs {
 // nothing and never synchronizes.
 extern "C" int fav4_bshd_forward_varlen(const Fav4VarlenArgs* args, int causal, hipStream_t stream);
 
+// Split-KV of packed sequences (no counterpart in the reference): the decode
+// step of continuous batching, each sequence with 1-32 new queries and its own
+// cache length.  For max_seqlen_q <= 32 and causal = 0 the query heads that
+// share a K/V head are packed into 32-row tiles (row = head-in-group *
+// max_seqlen_q + query) and every sequence's keys are cut into chunks of one
+// common number of key tiles (a sequence gets as many chunks as its keys
+// need), merged by their log-sum-exp as in fav4_bshd_forward_splitkv_gqa;
+// with equal lengths the result is bitwise that call's on the same data at
+// the same chunk count.  Anything else (max_seqlen_q > 32, or causal = 1:
+// top-left causal decode sees at most 32 keys) takes one chunk, i.e. runs
+// fav4_bshd_forward_varlen, and needs no workspace.  Same argument contract
+// as fav4_bshd_forward_varlen (O and LSE rows, empty sequences, offset
+// clamping), plus:
+//  * splits: 0 = library choice (the chunk size the contiguous split-KV Auto
+//    plan gives at the mean key length total_k / batch, enlarged so that the
+//    longest sequence needs at most 256 chunks), else 1..256 chunks of the
+//    longest sequence (clamped to its key tiles);
+//  * workspace as for fav4_bshd_forward_splitkv, of
+//    fav4_bshd_splitkv_varlen_workspace_size() bytes;
+//  * (heads / kv_heads) * max_seqlen_q < 2^23.
+// The two queries read only the sizes (pointers may be NULL) and return -1
+// for rejected arguments.
+extern "C" int fav4_bshd_forward_splitkv_varlen(const Fav4VarlenArgs* args, int causal, int splits,
+                                                void* workspace, size_t workspace_bytes, hipStream_t stream);
+extern "C" long long fav4_bshd_splitkv_varlen_workspace_size(const Fav4VarlenArgs* args, int causal, int splits);
+extern "C" int fav4_bshd_splitkv_varlen_select(const Fav4VarlenArgs* args, int causal);
+
 // ---- Arbitrary strides -----------------------------------------------------
 // No counterpart in the reference.  Q / O are read as [B, Sq, H, 128] and K /
 // V as [B, Sk, kv_heads, 128] views with the element (BF16) strides given per

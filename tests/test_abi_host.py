@@ -48,7 +48,9 @@ def test_exports_exactly_the_c_abi():
     assert public == {"fav4_bshd_forward", "fav4_bshd_select_config", "fav4_bshd_forward_splitkv",
                       "fav4_bshd_splitkv_workspace_size", "fav4_bshd_splitkv_select", "fav4_bshd_forward_gqa",
                       "fav4_bshd_forward_varlen", "fav4_bshd_forward_strided", "fav4_bshd_forward_splitkv_gqa",
-                      "fav4_bshd_splitkv_gqa_workspace_size", "fav4_bshd_splitkv_gqa_select"}, public
+                      "fav4_bshd_splitkv_gqa_workspace_size", "fav4_bshd_splitkv_gqa_select",
+                      "fav4_bshd_forward_splitkv_varlen", "fav4_bshd_splitkv_varlen_workspace_size",
+                      "fav4_bshd_splitkv_varlen_select"}, public
 
 
 def test_ctypes_layout_matches_reference(Args):
@@ -321,6 +323,90 @@ def test_varlen_rejects_bad_causal(lib, causal):
     a = load_package().VarlenArgs(**_vgood())
     assert lib.fav4_bshd_forward_varlen(C.byref(a), causal, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fav4_bshd_forward_varlen(None, 0, None) == HIP_ERROR_INVALID_VALUE
+
+
+# ---- split-KV of packed sequences --------------------------------------------
+def _varlen_split_plan(batch, h, kvh, max_q, max_k, total_k, splits, causal=False, cus=256):
+    """Closed form of the packed-batch plan: one chunk for max_q > 32; explicit
+    counts as the contiguous plan at the max lengths; Auto takes the chunk size
+    (key tiles) of the contiguous Auto plan at the mean key length, enlarged to
+    keep the longest sequence within 256 chunks."""
+    if max_q > 32:
+        return 1, 1
+    if splits:
+        return _split_plan(batch, h, max_q, max_k, splits, causal=causal, kvh=kvh)
+    mean = max(1, min(max_k, -(-total_k // batch)))
+    ktiles = -(-(min(max_k, max_q) if causal else max_k) // 32)
+    tps = max(_split_plan(batch, h, max_q, mean, 0, cus=cus, causal=causal, kvh=kvh)[1], -(-ktiles // 256))
+    return -(-ktiles // tps), tps
+
+
+def _vshape(batch, h, kvh, max_q, max_k, total_q, total_k):
+    f = _vgood()
+    f.update(q=None, k=None, v=None, o=None, cu_seqlens_q=None, cu_seqlens_k=None, batch=batch, heads=h,
+             kv_heads=kvh, max_seqlen_q=max_q, max_seqlen_k=max_k, total_q=total_q, total_k=total_k)
+    return load_package().VarlenArgs(**f)
+
+
+@pytest.mark.parametrize("shape", [(8, 32, 8, 1, 32768, 8 * 4096), (4, 8, 8, 1, 65536, 4 * 65536),
+                                   (3, 12, 3, 5, 4000, 5000), (16, 8, 1, 32, 9000, 16 * 300),
+                                   (2, 4, 2, 33, 8192, 8192), (1, 2, 2, 1, 31, 31), (5, 6, 2, 17, 2048, 3)])
+def test_splitkv_varlen_plan(lib, shape):
+    """Select and workspace queries of the packed-batch split-KV (shape only,
+    no buffers) against the closed form; explicit counts too."""
+    b, h, kvh, mq, mk, tk = shape
+    a = _vshape(b, h, kvh, mq, mk, b * mq, tk)
+    for causal in (0, 1):
+        n, _ = _varlen_split_plan(b, h, kvh, mq, mk, tk, 0, causal=bool(causal))
+        assert lib.fav4_bshd_splitkv_varlen_select(C.byref(a), causal) == n
+        want = 0 if n == 1 else n * b * h * mq * (128 * 4 + 8)
+        assert lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), causal, 0) == want
+        for req in (1, 3, 200, 256):
+            n, _ = _varlen_split_plan(b, h, kvh, mq, mk, tk, req, causal=bool(causal))
+            want = 0 if n == 1 else n * b * h * mq * (128 * 4 + 8)
+            assert lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), causal, req) == want
+
+
+def test_splitkv_varlen_plan_examples():
+    # 8 sequences of 4096 keys on average, one as long as 32768, 32 query heads
+    # over 8 K/V heads: 12 chunks of 11 tiles fill the CUs at the mean length,
+    # and the longest sequence needs 94 of them.
+    assert _varlen_split_plan(8, 32, 8, 1, 32768, 8 * 4096, 0, cus=256) == (94, 11)
+    # uniform lengths: the contiguous plan
+    for sk in (32768, 9 * 32 * 4, 1000, 77777):
+        assert _varlen_split_plan(4, 32, 8, 1, sk, 4 * sk, 0) == _split_plan(4, 32, 1, sk, 0, cus=256, kvh=8)
+    # one sequence far longer than the mean: chunks grow to stay within 256
+    assert _varlen_split_plan(64, 8, 8, 1, 1 << 20, 64 * 2048, 0, cus=256) == (256, 128)
+    assert _varlen_split_plan(2, 4, 2, 33, 8192, 8192, 0) == (1, 1)
+
+
+@pytest.mark.parametrize("name,change", VBAD + [("splits_neg", dict()), ("splits_big", dict())],
+                         ids=[b[0] for b in VBAD] + ["splits_neg", "splits_big"])
+def test_splitkv_varlen_rejects_bad_arguments(lib, name, change):
+    VarlenArgs = load_package().VarlenArgs
+    f = _vgood()
+    f["max_seqlen_q"] = 16          # the decode shape that splits
+    f.update(change)
+    if name == "grid_overflow":     # 2^35 partial rows
+        f.update(max_seqlen_q=32, max_seqlen_k=64)
+    splits = -1 if name == "splits_neg" else 257 if name == "splits_big" else 4
+    a = VarlenArgs(**f)
+    assert lib.fav4_bshd_forward_splitkv_varlen(C.byref(a), 0, splits, 0x100000, 1 << 40, None) == \
+        HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_forward_splitkv_varlen(None, 0, splits, 0x100000, 1 << 40, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_forward_splitkv_varlen(C.byref(a), 2, 4, 0x100000, 1 << 40, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_splitkv_varlen_select(None, 0) == -1
+    assert lib.fav4_bshd_splitkv_varlen_workspace_size(None, 0, 0) == -1
+
+
+@pytest.mark.parametrize("ws,nbytes", [(None, 1 << 30), (0x100010, 1 << 30), (0x100000, 1000)],
+                         ids=["null", "misaligned", "too_small"])
+def test_splitkv_varlen_rejects_workspace(lib, ws, nbytes):
+    VarlenArgs = load_package().VarlenArgs
+    f = _vgood()
+    f.update(max_seqlen_q=1, max_seqlen_k=8192, total_q=3, total_k=9000)
+    a = VarlenArgs(**f)
+    assert lib.fav4_bshd_forward_splitkv_varlen(C.byref(a), 0, 8, ws, nbytes, None) == HIP_ERROR_INVALID_VALUE
 
 
 # ---- arbitrary strides -------------------------------------------------------
