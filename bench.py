@@ -62,7 +62,7 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     p.add_argument("--sweep", default="", help="comma list of extra sequence lengths to time (report only)")
     p.add_argument("--no-comparator", action="store_true", help="skip the torch SDPA comparator")
-    p.add_argument("--no-splitkv", action="store_true", help="skip the split-KV report (B1 H8 Sq1024 Sk32768)")
+    p.add_argument("--no-splitkv", action="store_true", help="skip the split-KV report (B1 H8 Sq1024 Sk32768; B1 H1 S16384 causal)")
     p.add_argument("--no-api", action="store_true", help="skip the GQA / varlen report")
     p.add_argument("--no-telemetry", action="store_true",
                    help="start no child processes (amd-smi clocks, hipcc version), e.g. under a profiler")
@@ -281,24 +281,28 @@ def comparator(torch, orc, runner, q, k, v, o, stream, args, causal_list):
     return out
 
 
-def splitkv_report(torch, orc, runner, args, stream, b=1, h=8, sq=1024, sk=32768):
+def splitkv_report(torch, orc, runner, args, stream):
     """Few (b, h, q tile) items and long keys: the single-pass forward against the
     split-KV forward (Auto chunk count), both graph-timed, each output checked on
-    sampled rows first."""
+    sampled rows first.  B1 H8 Sq1024 Sk32768 dense and causal (causal rows see
+    only the first 1024 keys: Auto keeps the unsplit forward there), and a
+    single-head causal prefill of 16384 tokens."""
     g = torch.Generator(device="cuda")
     g.manual_seed(11939)
-    mk = lambda s: torch.randn((b, s, h, 128), device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
-    q, k, v = mk(sq), mk(sk), mk(sk)
-    o = torch.empty_like(q)
-    out = {"workload": f"B{b} H{h} Sq={sq} Sk={sk} D128 BF16, LSE off"}
-    for causal in (False, True):
+    out = {}
+    for label, b, h, sq, sk, causal in (("dense", 1, 8, 1024, 32768, False), ("causal", 1, 8, 1024, 32768, True),
+                                        ("causal_long", 1, 1, 16384, 16384, True)):
+        mk = lambda s: torch.randn((b, s, h, 128), device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
+        q, k, v = mk(sq), mk(sk), mk(sk)
+        o = torch.empty_like(q)
         splits = runner.splitkv_select(b, h, sq, sk, causal)
         ws = torch.empty(max(runner.splitkv_workspace_size(b, h, sq, sk, causal, 0), 1), device="cuda",
                          dtype=torch.uint8)
         plain = lambda: runner.call(q, k, v, o, None, causal, 0, stream=stream.cuda_stream)
         split = lambda: runner.call_splitkv(q, k, v, o, None, causal, 0, workspace=ws, stream=stream.cuda_stream)
         flop = orc.flops(b, h, sq, sk, causal)
-        res = {"splits": splits, "workspace_bytes": ws.numel()}
+        res = {"workload": f"B{b} H{h} Sq={sq} Sk={sk} D128 BF16 {'causal' if causal else 'dense'}, LSE off",
+               "splits": splits, "workspace_bytes": ws.numel()}
         for name, fn in (("plain", plain), ("splitkv", split)):
             o.fill_(float("nan"))
             torch.cuda.synchronize()   # the fill runs on the default stream
@@ -307,16 +311,15 @@ def splitkv_report(torch, orc, runner, args, stream, b=1, h=8, sq=1024, sk=32768
             torch.cuda.synchronize()
             err, _ = check_rows(torch, orc, q, k, v, o, causal, [(0, 0), (0, h - 1)])
             if not orc.check_acceptance_tolerance(err):
-                raise SystemExit(f"split-KV report: {name} check failed (causal={causal}): {err}")
-            us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream))
+                raise SystemExit(f"split-KV report: {name} check failed ({label}): {err}")
+            us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
             res[name] = dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1))
         res["speedup"] = round(res["plain"]["us"] / res["splitkv"]["us"], 2)
-        out["causal" if causal else "dense"] = res
+        out[label] = res
         print(f"# splitkv B{b} H{h} {sq}x{sk} causal={causal}: plain {res['plain']['tflops']} TFLOP/s, "
               f"split-KV ({splits} chunks) {res['splitkv']['tflops']} TFLOP/s, x{res['speedup']}",
               file=sys.stderr, flush=True)
-        del ws
-    del q, k, v, o
+        del q, k, v, o, ws
     torch.cuda.empty_cache()
     return out
 

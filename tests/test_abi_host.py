@@ -158,9 +158,31 @@ def _split_plan(b, h, sq, sk, splits, cus=None, causal=False, kvh=None):
     if splits == 0:
         items = b * kvh * -(-(h // kvh) * sq // bm) if sq <= 32 else b * h * -(-sq // bm)
         splits = min(-(-(cus * per_cu) // items), min(amax, max(1, ktiles // 4)))
+        if causal and sq > 32 and splits > 1:
+            splits = _causal_auto(b, h, sq, sk, splits, ktiles, cus)
     splits = max(1, min(splits, ktiles))
     tps = -(-ktiles // splits)
     return -(-ktiles // tps), tps
+
+
+def _causal_auto(b, h, sq, sk, max_splits, ktiles, cus):
+    """Causal prefill Auto: the count in 1..max_splits with the lowest predicted
+    time -- unsplit: rounds of 128-row tile pairs (2 per CU) x (9 + 1.0 per
+    64-key tile of the heaviest pair); split: rounds of (256-row q tile, chunk)
+    items (1 per CU) x (18 + 1.5 per tile of a chunk) + 5."""
+    keys = min(sk, sq)
+    vis = lambda end: -(-min(keys, end) // 64)
+    nt128 = -(-sq // 128)
+    npairs = (nt128 + 1) // 2
+    heavy = max(vis(128 * (i + 1)) + (vis(128 * (nt128 - i)) if nt128 - 1 - i != i else 0) for i in range(npairs))
+    best, pick = -(-(b * h * npairs) // (2 * cus)) * (9.0 + heavy), 1
+    for s in range(2, max_splits + 1):
+        tps = -(-ktiles // s)
+        items = sum(-(-vis(256 * (i + 1)) // tps) for i in range(-(-sq // 256)))
+        t = -(-(b * h * items) // cus) * (18.0 + 1.5 * tps) + 5.0
+        if t < best:
+            best, pick = t, s
+    return pick
 
 
 @pytest.mark.parametrize("shape,splits", [((2, 3, 300, 5000), 5), ((1, 8, 1024, 32768), 16), ((1, 1, 1, 64), 8),
@@ -175,7 +197,8 @@ def test_splitkv_workspace_size_closed_form(lib, Args, shape, splits):
 
 
 @pytest.mark.parametrize("shape", [(1, 8, 1024, 32768), (32, 8, 4096, 4096), (1, 1, 256, 65536), (2, 4, 512, 2048),
-                                   (1, 1, 100, 100)])
+                                   (1, 1, 100, 100), (1, 8, 2048, 32768), (1, 8, 4096, 32768), (1, 16, 2048, 2048),
+                                   (1, 2, 8192, 4000), (1, 1, 16384, 16384), (3, 2, 1500, 60000)])
 def test_splitkv_auto_plan(lib, Args, shape):
     """Auto chunk count, for the CU count the library sees (256 on MI355X; the
     same fallback when no device is visible)."""
@@ -200,8 +223,14 @@ def test_splitkv_plan_examples():
     assert _split_plan(32, 8, 4096, 4096, 0, cus=256)[0] == 1
     assert _split_plan(2, 3, 300, 5000, 5) == (5, 16)
     assert _split_plan(1, 1, 256, 65536, 0, cus=256) == (64, 16)
-    # causal B1 H8 Sq1024 Sk32768 sees only the first 1024 keys: 4 chunks of 4 tiles
-    assert _split_plan(1, 8, 1024, 32768, 0, cus=256, causal=True) == (4, 4)
+    # causal prefill: the model keeps the unsplit forward where splitting
+    # measured slower (Sq1024 H8, Sq2048 H16, Sq512) and splits where it won
+    # (Sq2048 H8: 4 chunks, 36 vs 43 us; Sq4096 H8: 2 chunks, 70 vs 75 us)
+    assert _split_plan(1, 8, 1024, 32768, 0, cus=256, causal=True)[0] == 1
+    assert _split_plan(1, 16, 2048, 2048, 0, cus=256, causal=True)[0] == 1
+    assert _split_plan(1, 8, 512, 65536, 0, cus=256, causal=True)[0] == 1
+    assert _split_plan(1, 8, 2048, 32768, 0, cus=256, causal=True) == (4, 8)
+    assert _split_plan(1, 8, 4096, 32768, 0, cus=256, causal=True) == (2, 32)
     # GQA decode B4 H32 KVH8 Sq1 Sk32768: 4 heads of a group share one 32-row
     # tile, 32 items, 1024 key tiles -> 24 chunks of 43
     assert _split_plan(4, 32, 1, 32768, 0, cus=256, kvh=8) == (24, 43)

@@ -93,7 +93,8 @@ def test_splitkv_single_chunk_is_the_plain_forward(gpu_runner):
 @pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
 def test_splitkv_long_keys_sampled_rows(gpu_runner, causal):
     """The shape split-KV is for: B1 H8 Sq1024 Sk32768 (32 q tiles; Auto -> 8 chunks
-    dense, 4 causal, where rows see only the first 1024 keys), checked on the
+    dense; causal rows see only the first 1024 keys, where Auto keeps the
+    unsplit forward, so causal runs 4 explicit chunks), checked on the
     reference's sampled rows for every head."""
     import torch
     g = torch.Generator(device="cuda")
@@ -102,9 +103,10 @@ def test_splitkv_long_keys_sampled_rows(gpu_runner, causal):
     q, k, v = mk(1024), mk(32768), mk(32768)
     o = torch.full_like(q, float("nan"))
     lse = torch.full((1, 8, 1024), float("nan"), device="cuda", dtype=torch.float32)
-    assert gpu_runner.splitkv_select(1, 8, 1024, 32768, causal) == (4 if causal else 8)
-    print(f"  splitkv B1 H8 1024x32768 causal={causal} auto", flush=True)
-    gpu_runner.call_splitkv(q, k, v, o, lse, causal, 0)
+    assert gpu_runner.splitkv_select(1, 8, 1024, 32768, causal) == (1 if causal else 8)
+    splits = 4 if causal else 0
+    print(f"  splitkv B1 H8 1024x32768 causal={causal} splits={splits}", flush=True)
+    gpu_runner.call_splitkv(q, k, v, o, lse, causal, splits)
     torch.cuda.synchronize()
     assert not torch.isnan(o).any().item()
     rows = orc.sample_rows(1024)
