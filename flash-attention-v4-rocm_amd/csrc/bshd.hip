@@ -119,38 +119,49 @@ int device_cus() {
     return cus;
 }
 
-// Auto for top-left causal prefill.  Filling the CUs is not enough here: the
-// unsplit forward pairs a heavy q tile with a light one, the split kernel
-// runs every (q tile, chunk) on its own, with higher fixed costs.  Auto
-// therefore keeps, among 1..max_splits chunks, the count with the lowest
-// predicted time.  The model (microseconds; fitted to graph-timed MI355X runs
-// of B1 H8-16 causal, Sq 512-4096, Sk up to 65536, where it picks the fastest
-// measured choice every time):
-//  * unsplit (Auto config 1 on these grids: pairs of 128-row q tiles, two
-//    workgroups per CU): rounds * (9 + 1.0 per 64-key tile of the heaviest
-//    pair);
-//  * split (256-row q tiles, one workgroup per CU): rounds * (18 + 1.5 per
-//    64-key tile of a chunk) + 5 for the merge;
+// Auto for prefill (Sq > 32).  Filling the CUs is not enough: on the small
+// grids where splitting is considered, the unsplit forward runs 128-row q
+// tiles two per CU (causal: a heavy tile paired with a light one), while the
+// split kernel runs 256-row (q tile, chunk) items one per CU with higher fixed
+// costs.  Auto therefore keeps, among 1..max_splits chunks, the count with
+// the lowest predicted time.  The model (microseconds; fitted to graph-timed
+// MI355X runs of 23 shapes, B1-4, H1-64, Sq 256-16384, Sk up to 65536, where
+// it picks the fastest measured choice or one within 2% of it):
+//  * unsplit: rounds * (9 + c per 64-key tile of an item), an item being a
+//    q tile (dense; c = 0.9 with at most one workgroup per CU, else 1.0) or
+//    the heaviest tile pair (causal; c = 1.0);
+//  * split: rounds * (F + c per 64-key tile of a chunk) + 5 for the merge,
+//    F = 19 and c = 1.8 dense, F = 18 and c = 1.5 causal;
 // where rounds = work items / resident workgroups, rounded up.
-int causal_auto_splits(const Fav4Args& a, int max_splits, int ktiles) {
+int prefill_auto_splits(const Fav4Args& a, int causal, int max_splits, int ktiles) {
     const int64_t cus = device_cus();
     const int64_t bh = int64_t(a.batch) * a.heads;
-    const int keys = std::min(a.sk, a.sq);
-    auto vis_tiles = [&](int64_t rows_end) { return int((std::min<int64_t>(keys, rows_end) + 63) / 64); };
-    const int nt128 = (a.sq + 127) / 128, npairs = (nt128 + 1) / 2;
-    int heavy = 0;
-    for (int i = 0; i < npairs; ++i) {
-        const int j = nt128 - 1 - i;
-        heavy = std::max(heavy, vis_tiles(128LL * (i + 1)) + (j != i ? vis_tiles(128LL * (j + 1)) : 0));
+    const int keys = causal ? std::min(a.sk, a.sq) : a.sk;
+    auto vis_tiles = [&](int64_t rows_end) {
+        return int((std::min<int64_t>(keys, causal ? rows_end : keys) + 63) / 64);
+    };
+    const int nt128 = (a.sq + 127) / 128;
+    double best;
+    if (causal) {
+        const int npairs = (nt128 + 1) / 2;
+        int heavy = 0;
+        for (int i = 0; i < npairs; ++i) {
+            const int j = nt128 - 1 - i;
+            heavy = std::max(heavy, vis_tiles(128LL * (i + 1)) + (j != i ? vis_tiles(128LL * (j + 1)) : 0));
+        }
+        best = double((bh * npairs + 2 * cus - 1) / (2 * cus)) * (9.0 + 1.0 * heavy);
+    } else {
+        const int64_t items = bh * nt128;
+        best = double((items + 2 * cus - 1) / (2 * cus)) * (9.0 + (items <= cus ? 0.9 : 1.0) * ktiles);
     }
-    double best = double((bh * npairs + 2 * cus - 1) / (2 * cus)) * (9.0 + 1.0 * heavy);
+    const double fixed = causal ? 18.0 : 19.0, per_tile = causal ? 1.5 : 1.8;
     int pick = 1;
     const int nt256 = (a.sq + 255) / 256;
     for (int s = 2; s <= max_splits; ++s) {
         const int tps = (ktiles + s - 1) / s;
         int64_t items = 0;
         for (int i = 0; i < nt256; ++i) items += (vis_tiles(256LL * (i + 1)) + tps - 1) / tps;
-        const double t = double((bh * items + cus - 1) / cus) * (18.0 + 1.5 * tps) + 5.0;
+        const double t = double((bh * items + cus - 1) / cus) * (fixed + per_tile * tps) + 5.0;
         if (t < best) best = t, pick = s;
     }
     return pick;
@@ -159,7 +170,7 @@ int causal_auto_splits(const Fav4Args& a, int max_splits, int ktiles) {
 // Chunking of the key range a row can see (top-left causal never shows a key
 // past sq - 1); `req` = 0 picks enough chunks to fill the CUs once (the
 // shape's resident workgroups per CU; more chunks only add merge traffic and
-// per-chunk pipeline fill), for causal prefill then the model above.  The
+// per-chunk pipeline fill), for prefill then the model above.  The
 // count is then rounded so that no chunk starts past that range.
 // The decode shape packs the query heads that share a K/V head into one row
 // space of (heads / kv_heads) * sq rows per (batch, K/V head).
@@ -176,7 +187,7 @@ SplitPlan split_plan(const Fav4Args& a, int kv_heads, int causal, int req) {
         const int64_t units = items * tiles;
         splits = (int64_t(device_cus()) * sh.wgs_per_cu + units - 1) / units;
         splits = std::min<int64_t>(splits, std::min(sh.auto_max, std::max(1, ktiles / MIN_TILES_PER_SPLIT)));
-        if (causal && !pack && splits > 1) splits = causal_auto_splits(a, int(splits), ktiles);
+        if (!pack && splits > 1) splits = prefill_auto_splits(a, causal, int(splits), ktiles);
     }
     splits = std::max<int64_t>(1, std::min<int64_t>(splits, ktiles));
     const int tps = int((ktiles + splits - 1) / splits);

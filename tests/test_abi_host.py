@@ -158,28 +158,37 @@ def _split_plan(b, h, sq, sk, splits, cus=None, causal=False, kvh=None):
     if splits == 0:
         items = b * kvh * -(-(h // kvh) * sq // bm) if sq <= 32 else b * h * -(-sq // bm)
         splits = min(-(-(cus * per_cu) // items), min(amax, max(1, ktiles // 4)))
-        if causal and sq > 32 and splits > 1:
-            splits = _causal_auto(b, h, sq, sk, splits, ktiles, cus)
+        if sq > 32 and splits > 1:
+            splits = _prefill_auto(b, h, sq, sk, causal, splits, ktiles, cus)
     splits = max(1, min(splits, ktiles))
     tps = -(-ktiles // splits)
     return -(-ktiles // tps), tps
 
 
-def _causal_auto(b, h, sq, sk, max_splits, ktiles, cus):
-    """Causal prefill Auto: the count in 1..max_splits with the lowest predicted
-    time -- unsplit: rounds of 128-row tile pairs (2 per CU) x (9 + 1.0 per
-    64-key tile of the heaviest pair); split: rounds of (256-row q tile, chunk)
-    items (1 per CU) x (18 + 1.5 per tile of a chunk) + 5."""
-    keys = min(sk, sq)
-    vis = lambda end: -(-min(keys, end) // 64)
+def _prefill_auto(b, h, sq, sk, causal, max_splits, ktiles, cus):
+    """Prefill Auto: the count in 1..max_splits with the lowest predicted time --
+    unsplit: rounds of 128-row q tiles (causal: tile pairs), 2 per CU, x (9 +
+    c per 64-key tile of a q tile, c = 0.9 with <= 1 workgroup per CU else 1.0;
+    causal: 1.0 per tile of the heaviest pair); split: rounds of (256-row q
+    tile, chunk) items, 1 per CU, x (19 + 1.8 per tile of a chunk; causal 18 +
+    1.5) + 5."""
+    keys = min(sk, sq) if causal else sk
+    vis = lambda end: -(-min(keys, end if causal else keys) // 64)
     nt128 = -(-sq // 128)
-    npairs = (nt128 + 1) // 2
-    heavy = max(vis(128 * (i + 1)) + (vis(128 * (nt128 - i)) if nt128 - 1 - i != i else 0) for i in range(npairs))
-    best, pick = -(-(b * h * npairs) // (2 * cus)) * (9.0 + heavy), 1
+    if causal:
+        npairs = (nt128 + 1) // 2
+        heavy = max(vis(128 * (i + 1)) + (vis(128 * (nt128 - i)) if nt128 - 1 - i != i else 0)
+                    for i in range(npairs))
+        best = -(-(b * h * npairs) // (2 * cus)) * (9.0 + heavy)
+    else:
+        items = b * h * nt128
+        best = -(-items // (2 * cus)) * (9.0 + (0.9 if items <= cus else 1.0) * ktiles)
+    fixed, per_tile = (18.0, 1.5) if causal else (19.0, 1.8)
+    pick = 1
     for s in range(2, max_splits + 1):
         tps = -(-ktiles // s)
         items = sum(-(-vis(256 * (i + 1)) // tps) for i in range(-(-sq // 256)))
-        t = -(-(b * h * items) // cus) * (18.0 + 1.5 * tps) + 5.0
+        t = -(-(b * h * items) // cus) * (fixed + per_tile * tps) + 5.0
         if t < best:
             best, pick = t, s
     return pick
