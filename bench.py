@@ -449,8 +449,50 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
         res[name] = {"us": round(us, 2), "kv_tbps": round(kv_bytes / us / 1e6, 2)}
         print(f"# varlen decode {name}: {us:.1f} us, K+V {kv_bytes / us / 1e6:.2f} TB/s", file=sys.stderr, flush=True)
     res["speedup"] = round(res["plain"]["us"] / res["splitkv"]["us"], 2)
+
+    # The same decode batch over paged K/V caches: 64-key pages in a random
+    # order, Auto chunk count; checked like the packed run.
+    ps = 64
+    npg = [-(-int(n) // ps) for n in klens]
+    perm = torch.randperm(sum(npg), generator=torch.Generator().manual_seed(5)).cuda()
+    kc = torch.zeros((sum(npg), ps, vkvh, 128), device="cuda", dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    table = torch.zeros((vb, max(npg)), device="cuda", dtype=torch.int32)
+    at = 0
+    for i, n in enumerate(npg):
+        ids = perm[at:at + n]
+        at += n
+        table[i, :n] = ids.to(torch.int32)
+        ks, ke = int(cuk_h[i]), int(cuk_h[i + 1])
+        for src, dst in ((k, kc), (v, vc)):
+            pad = torch.zeros((n * ps, vkvh, 128), device="cuda", dtype=torch.bfloat16)
+            pad[:ke - ks] = src[ks:ke]
+            dst[ids] = pad.view(n, ps, vkvh, 128)
+    seqlens = torch.from_numpy(klens.astype(np.int32)).cuda()
+    pws = torch.empty(max(runner.splitkv_paged_workspace_size(vb, vh, vkvh, 1, mk_len, vb, tk, ps, max(npg), sum(npg)),
+                          256), device="cuda", dtype=torch.uint8)
+    fn = lambda: runner.call_splitkv_paged(q, kc, vc, o, None, cuq, seqlens, table, 1, mk_len, 0, workspace=pws,
+                                           total_k=tk, stream=stream.cuda_stream)
+    o.fill_(float("nan"))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        fn()
+    torch.cuda.synchronize()
+    for i in (0, int(np.argmax(klens))):
+        ks, ke = int(cuk_h[i]), int(cuk_h[i + 1])
+        err, _ = check_rows(torch, orc, q[i:i + 1][None], k[ks:ke][None].repeat_interleave(grp, dim=2),
+                            v[ks:ke][None].repeat_interleave(grp, dim=2), o[i:i + 1][None], False,
+                            [(0, 0), (0, vh - 1)])
+        if not orc.check_acceptance_tolerance(err):
+            raise SystemExit(f"api report: paged decode check failed: {err}")
+    us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+    res["paged"] = {"page_size": ps, "splits": runner.splitkv_paged_select(vb, vh, vkvh, 1, mk_len, vb, tk, ps,
+                                                                            max(npg), sum(npg)),
+                    "us": round(us, 2), "kv_tbps": round(kv_bytes / us / 1e6, 2)}
+    print(f"# varlen decode paged ({ps}-key pages): {us:.1f} us, K+V {kv_bytes / us / 1e6:.2f} TB/s", file=sys.stderr,
+          flush=True)
     out["varlen_decode"] = res
-    del q, k, v, o, ws
+    del q, k, v, o, ws, kc, vc, pws
     torch.cuda.empty_cache()
     return out
 

@@ -219,13 +219,14 @@ int split_args_ok(const Fav4Args* a, int kv_heads, int causal, int splits) {
 }
 
 // VARLEN: `a` holds the packed batch's shape (max lengths) and `sp` its
-// sequence offsets; decode shape only.  Top-left causal decode (sq <= 32) sees
-// at most 32 keys, one tile, so the plan never splits it: causal launches use
-// the prefill shape only.
-template <bool CAUSAL, bool VARLEN = false>
+// sequence offsets; decode shape only.  PAGED: the same over paged K/V caches.
+// Top-left causal decode (sq <= 32) sees at most 32 keys, one tile, so the
+// plan never splits it: causal launches use the prefill shape only.
+template <bool CAUSAL, bool VARLEN = false, bool PAGED = false>
 int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, fav4::SplitArgs sp,
                  hipStream_t stream) {
     static_assert(!(CAUSAL && VARLEN), "causal decode never splits");
+    static_assert(!PAGED || VARLEN, "paged caches hold packed sequences");
     const int tiles = p.tiles;
     const int64_t total = p.items * tiles * p.splits;
     const int64_t rows = int64_t(a.batch) * a.heads * a.sq;
@@ -241,8 +242,8 @@ int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, 
         hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, stream, a, sp, kv_heads, tiles, int(total));
     };
     if constexpr (VARLEN) {
-        if (a.lse) go(fav4::fwd_kernel_split<32, false, 1, true, true>, 64);
-        else go(fav4::fwd_kernel_split<32, false, 1, false, true>, 64);
+        if (a.lse) go(fav4::fwd_kernel_split<32, false, 1, true, true, PAGED>, 64);
+        else go(fav4::fwd_kernel_split<32, false, 1, false, true, PAGED>, 64);
     } else if constexpr (CAUSAL) {
         if (a.lse) go(fav4::fwd_kernel_split<64, true, 8, true>, 512);
         else go(fav4::fwd_kernel_split<64, true, 8, false>, 512);
@@ -321,19 +322,23 @@ Fav4Args varlen_shape(const Fav4VarlenArgs& v) {
 // would need more than MAX_SPLITS chunks: a ragged batch's long sequences
 // thus spread over as many workgroups as a uniform batch's, and a uniform
 // batch gets exactly the contiguous plan.
-SplitPlan varlen_split_plan(const Fav4VarlenArgs& v, int causal, int req) {
-    const Fav4Args a = varlen_shape(v);
+// `a` is the packed batch's shape (max lengths), total_k its key count.
+SplitPlan packed_split_plan(const Fav4Args& a, int kv_heads, int64_t total_k, int causal, int req) {
     if (a.sq > DECODE_SQ) return {1, 1, split_shape(a), 1, 1};
-    SplitPlan p = split_plan(a, v.kv_heads, causal, req == 0 ? 1 : req);
+    SplitPlan p = split_plan(a, kv_heads, causal, req == 0 ? 1 : req);
     if (req == 0) {
         Fav4Args mean = a;
-        mean.sk = int(std::max<int64_t>(1, std::min<int64_t>(a.sk, (int64_t(v.total_k) + v.batch - 1) / v.batch)));
+        mean.sk = int(std::max<int64_t>(1, std::min<int64_t>(a.sk, (total_k + a.batch - 1) / a.batch)));
         const int keys = causal ? std::min(a.sk, a.sq) : a.sk;
         const int ktiles = (keys + p.shape.bn - 1) / p.shape.bn;
-        p.tps = std::max(split_plan(mean, v.kv_heads, causal, 0).tps, (ktiles + fav4::MAX_SPLITS - 1) / fav4::MAX_SPLITS);
+        p.tps = std::max(split_plan(mean, kv_heads, causal, 0).tps, (ktiles + fav4::MAX_SPLITS - 1) / fav4::MAX_SPLITS);
         p.splits = (ktiles + p.tps - 1) / p.tps;
     }
     return p;
+}
+
+SplitPlan varlen_split_plan(const Fav4VarlenArgs& v, int causal, int req) {
+    return packed_split_plan(varlen_shape(v), v.kv_heads, v.total_k, causal, req);
 }
 
 int varlen_split_ok(const Fav4VarlenArgs* v, int causal, int splits, bool buffers) {
@@ -343,6 +348,63 @@ int varlen_split_ok(const Fav4VarlenArgs* v, int causal, int splits, bool buffer
     if (v->max_seqlen_q > DECODE_SQ) return hipSuccess;
     const Fav4Args a = varlen_shape(*v);
     return split_shape_ok(&a, v->kv_heads, causal, splits);
+}
+
+// ---- paged K/V caches ----------------------------------------------------
+constexpr int PAGED_MAX_TPS = 64;          // key tiles per chunk: one page number per lane
+constexpr int PAGED_MAX_KEYS = fav4::MAX_SPLITS * PAGED_MAX_TPS * 32;
+
+int paged_shape_ok(const Fav4PagedArgs* a, int causal, int splits) {
+    if (!a || a->batch <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads != 0 ||
+        a->max_seqlen_q <= 0 || a->max_seqlen_q > DECODE_SQ || a->max_seqlen_k <= 0 || a->total_q <= 0 ||
+        a->total_k < 0 || a->num_pages <= 0 || a->page_size <= 0 || a->page_size % 32 != 0 ||
+        a->max_pages_per_seq <= 0 || causal != 0 || !std::isfinite(a->scale) || a->scale <= 0 || splits < 0 ||
+        splits > fav4::MAX_SPLITS)
+        return hipErrorInvalidValue;
+    if (a->batch > INT_MAX - 1 || a->heads > INT_MAX / 256 || a->max_seqlen_k > PAGED_MAX_KEYS ||
+        int64_t(a->max_seqlen_k) > int64_t(a->max_pages_per_seq) * a->page_size ||
+        int64_t(a->page_size) * a->kv_heads * 256 > int64_t(UINT32_MAX) ||
+        int64_t(a->max_seqlen_q) * a->heads * 256 > int64_t(UINT32_MAX) ||
+        int64_t(a->heads / a->kv_heads) * a->max_seqlen_q * fav4::D * 4 > int64_t(UINT32_MAX) ||
+        int64_t(a->batch) * a->heads * a->max_seqlen_q > INT_MAX)
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+int paged_ok(const Fav4PagedArgs* a, int causal, int splits) {
+    if (paged_shape_ok(a, causal, splits) != hipSuccess || !a->q || !a->k_cache || !a->v_cache || !a->o ||
+        !a->cu_seqlens_q || !a->seqlens_k || !a->block_table ||
+        ((reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->k_cache) |
+          reinterpret_cast<uintptr_t>(a->v_cache) | reinterpret_cast<uintptr_t>(a->o)) & 15) ||
+        ((reinterpret_cast<uintptr_t>(a->cu_seqlens_q) | reinterpret_cast<uintptr_t>(a->seqlens_k) |
+          reinterpret_cast<uintptr_t>(a->block_table)) & 3) ||
+        (a->lse && (reinterpret_cast<uintptr_t>(a->lse) & 3)))
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+Fav4Args paged_shape(const Fav4PagedArgs& v) {
+    Fav4Args a{};
+    a.q = v.q; a.k = v.k_cache; a.v = v.v_cache; a.o = v.o; a.lse = v.lse;
+    a.batch = v.batch; a.heads = v.heads; a.sq = v.max_seqlen_q; a.sk = v.max_seqlen_k;
+    a.scale = v.scale;
+    return a;
+}
+
+// The packed-batch plan, with chunks capped at 64 key tiles (a chunk's page
+// numbers fit the lanes of one wave); one chunk still runs the split kernels.
+SplitPlan paged_plan(const Fav4PagedArgs& v, int req) {
+    SplitPlan p = packed_split_plan(paged_shape(v), v.kv_heads, v.total_k, 0, req);
+    if (p.tps > PAGED_MAX_TPS) {
+        const int ktiles = (v.max_seqlen_k + 31) / 32;
+        p.tps = PAGED_MAX_TPS;
+        p.splits = (ktiles + p.tps - 1) / p.tps;
+    }
+    return p;
+}
+
+int64_t paged_workspace(const Fav4PagedArgs& v, const SplitPlan& p) {
+    return int64_t(p.splits) * v.batch * v.heads * v.max_seqlen_q * (fav4::D * 4 + 2 * 4);
 }
 
 // Auto: 128-row workgroups (config 1; two per CU, so one's prologue and
@@ -520,4 +582,39 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_
     sp.total_q = a->total_q;
     sp.total_k = a->total_k;
     return launch_split<false, true>(shape, a->kv_heads, p, workspace, sp, stream);
+}
+
+// Split-KV decode over paged K/V caches (no counterpart in the reference).
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_splitkv_paged_select(const Fav4PagedArgs* a,
+                                                                             int causal) {
+    if (paged_shape_ok(a, causal, 0) != hipSuccess) return -1;
+    return paged_plan(*a, 0).splits;
+}
+
+extern "C" __attribute__((visibility("default"))) long long fav4_bshd_splitkv_paged_workspace_size(
+    const Fav4PagedArgs* a, int causal, int splits) {
+    if (paged_shape_ok(a, causal, splits) != hipSuccess) return -1;
+    return paged_workspace(*a, paged_plan(*a, splits));
+}
+
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_paged(const Fav4PagedArgs* a,
+                                                                              int causal, int splits,
+                                                                              void* workspace,
+                                                                              size_t workspace_bytes,
+                                                                              hipStream_t stream) {
+    const int st = paged_ok(a, causal, splits);
+    if (st != hipSuccess) return st;
+    const SplitPlan p = paged_plan(*a, splits);
+    const int64_t need = paged_workspace(*a, p);
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || uint64_t(need) > workspace_bytes)
+        return hipErrorInvalidValue;
+    fav4::SplitArgs sp{};
+    sp.cu_q = a->cu_seqlens_q;
+    sp.total_q = a->total_q;
+    sp.seqlens_k = a->seqlens_k;
+    sp.block_table = a->block_table;
+    sp.page_size = a->page_size;
+    sp.max_pages = a->max_pages_per_seq;
+    sp.num_pages = a->num_pages;
+    return launch_split<false, true, true>(paged_shape(*a), a->kv_heads, p, workspace, sp, stream);
 }

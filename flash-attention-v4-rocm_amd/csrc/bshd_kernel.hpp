@@ -584,20 +584,28 @@ struct SplitArgs {
     const int* cu_q;
     const int* cu_k;
     int total_q, total_k;
+    // Paged K/V caches (PAGED kernels): sequence b has seqlens_k[b] keys, key
+    // j in row block_table[b * max_pages + j / page_size] * page_size +
+    // j % page_size of the [num_pages * page_size, kv_heads, 128] caches.
+    const int* seqlens_k;
+    const int* block_table;
+    int page_size, max_pages, num_pages;
 };
 
-// Query / key count and first token of sequence b, read on the device and
-// clamped to [0, total] and to the max lengths, as fwd_kernel_varlen does.
-// UNIFORM: b is the same in every lane (the offsets then live in SGPRs).
+// Query / key count and first token of sequence b (the same in every lane of
+// the workgroup), read on the device and clamped to [0, total] and to the max
+// lengths, as fwd_kernel_varlen does.  PAGED: the key count is seqlens_k[b]
+// clamped to [0, max_k] (ktok unused).
 struct SeqSpan {
     int sq, sk;
     int64_t qtok, ktok;
 };
-template <bool UNIFORM>
+template <bool PAGED>
 __device__ __forceinline__ SeqSpan seq_span(const SplitArgs& sp, int b, int max_q, int max_k) {
-    auto rd = [](int x) { return UNIFORM ? __builtin_amdgcn_readfirstlane(x) : x; };
+    auto rd = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
     const int qs = min(max(rd(sp.cu_q[b]), 0), sp.total_q);
     const int qe = min(max(rd(sp.cu_q[b + 1]), qs), min(sp.total_q, qs + max_q));
+    if constexpr (PAGED) return {qe - qs, min(max(rd(sp.seqlens_k[b]), 0), max_k), qs, 0};
     const int ks = min(max(rd(sp.cu_k[b]), 0), sp.total_k);
     const int ke = min(max(rd(sp.cu_k[b + 1]), ks), min(sp.total_k, ks + max_k));
     return {qe - qs, ke - ks, qs, ks};
@@ -615,10 +623,14 @@ __device__ __forceinline__ SeqSpan seq_span(const SplitArgs& sp, int b, int max_
 // VARLEN: packed sequences (one wave only); a.sq / a.sk are the max lengths,
 // packed rows keep the a.sq stride, and rows past a sequence's own length are
 // computed on a valid query but never read by the merge.
-template <int BN, bool CAUSAL, int WAVES, bool LSE, bool VARLEN = false>
+// PAGED (with VARLEN): K/V come from paged caches.  page_size is a multiple
+// of BN, so a key tile lies in one page; a chunk spans at most 64 pages, whose
+// (clamped) numbers one load puts in the wave's lanes at the chunk start.
+template <int BN, bool CAUSAL, int WAVES, bool LSE, bool VARLEN = false, bool PAGED = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int total) {
     static_assert(!VARLEN || WAVES == 1, "packed sequences use the one-wave shape");
+    static_assert(!PAGED || VARLEN, "paged caches hold packed sequences");
     constexpr int BM = WAVES * 32, STAGES = 3;
     // One wave (decode): the q-tile rows are the group's query heads times
     // their sq queries, row r = (head - first head of the group) * sq + query,
@@ -686,7 +698,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
         // The sequence: its query / key counts and first tokens.
         SeqSpan span{a.sq, a.sk, int64_t(batch) * a.sq, int64_t(batch) * a.sk};
         if constexpr (VARLEN) {
-            span = seq_span<true>(sp, batch, a.sq, a.sk);
+            span = seq_span<PAGED>(sp, batch, a.sq, a.sk);
             if (span.sq == 0) continue;                        // no query rows: nothing to merge
         }
         const int sq = span.sq, sk = span.sk;
@@ -721,14 +733,29 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
         st.l = 0.f;
 
         if (t0 < t1) {
+            // PAGED: lane l holds the page of the chunk's l-th page slot.
+            int pages = 0, page0 = 0;
+            if constexpr (PAGED) {
+                page0 = t0 * BN / sp.page_size;
+                const int slot = min(page0 + lane, sp.max_pages - 1);
+                pages = min(max(sp.block_table[int64_t(batch) * sp.max_pages + slot], 0), sp.num_pages - 1);
+            }
             // DMA of key tile t into stage (t - t0) % 3.  Tiles past the chunk
             // are clamped to its last one (the copy lands in a stage no later
             // step reads), keeping the vmcnt count uniform.
             auto issue = [&](int t) {
-                const int64_t first = int64_t(min(t, t1 - 1)) * BN;
-                const uint32_t bytes = uint32_t(sk - int(first) - 1) * kv_row_bytes + ROW_BYTES;
-                const u32x4 rk = make_desc(kbase + first * kv_row_bytes, bytes);
-                const u32x4 rv = make_desc(vbase + first * kv_row_bytes, bytes);
+                const int first = min(t, t1 - 1) * BN;
+                int64_t row0 = first;                       // the tile's first K/V row
+                int rows_left = sk - first;                 // rows the descriptor may cover
+                if constexpr (PAGED) {
+                    const int in_page = first % sp.page_size;
+                    const int page = __builtin_amdgcn_readlane(pages, first / sp.page_size - page0);
+                    row0 = int64_t(page) * sp.page_size + in_page;
+                    rows_left = min(rows_left, sp.page_size - in_page);
+                }
+                const uint32_t bytes = uint32_t(rows_left - 1) * kv_row_bytes + ROW_BYTES;
+                const u32x4 rk = make_desc(kbase + row0 * kv_row_bytes, bytes);
+                const u32x4 rv = make_desc(vbase + row0 * kv_row_bytes, bytes);
                 const uint32_t ks = smem_base + ((t - t0) % STAGES) * STAGE_BYTES + wave * DMA * 1024;
 #pragma unroll
                 for (int i = 0; i < DMA; ++i) {
@@ -1040,9 +1067,11 @@ __global__ __launch_bounds__(256) void combine_kernel(Fav4Args a, SplitArgs sp) 
         bool live = r < rows;
         if constexpr (VARLEN) {
             if (live) {
-                const SeqSpan span = seq_span<false>(sp, batch, a.sq, a.sk);
-                live = qi < span.sq;
-                qtok = span.qtok + qi;
+                // Only the query side: paged batches have no key offsets.
+                const int qs = min(max(sp.cu_q[batch], 0), sp.total_q);
+                const int qe = min(max(sp.cu_q[batch + 1], qs), min(sp.total_q, qs + a.sq));
+                live = qi < qe - qs;
+                qtok = int64_t(qs) + qi;
             }
         }
         float vb[MAXV], vl[MAXV];

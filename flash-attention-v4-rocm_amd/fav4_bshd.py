@@ -44,6 +44,14 @@ class VarlenArgs(C.Structure):
                                "total_k")] + [("scale", C.c_float)]
 
 
+class PagedArgs(C.Structure):
+    """``struct Fav4PagedArgs`` (include/fav4_bshd.h): 8 pointers, 10 ints, 1 float."""
+    _fields_ = [(n, C.c_void_p) for n in ("q", "k_cache", "v_cache", "o", "lse", "cu_seqlens_q", "seqlens_k",
+                                          "block_table")] + [
+        (n, C.c_int) for n in ("batch", "heads", "kv_heads", "max_seqlen_q", "max_seqlen_k", "total_q", "total_k",
+                               "num_pages", "page_size", "max_pages_per_seq")] + [("scale", C.c_float)]
+
+
 class Strides(C.Structure):
     """``struct Fav4Strides`` (include/fav4_bshd.h): element strides of a [B, S, H, 128] view."""
     _fields_ = [(n, C.c_longlong) for n in ("batch", "seq", "head")]
@@ -106,6 +114,13 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
         lib.fav4_bshd_splitkv_varlen_workspace_size.restype = C.c_longlong
         lib.fav4_bshd_splitkv_varlen_select.argtypes = [C.POINTER(VarlenArgs), C.c_int]
         lib.fav4_bshd_splitkv_varlen_select.restype = C.c_int
+        lib.fav4_bshd_forward_splitkv_paged.argtypes = [C.POINTER(PagedArgs), C.c_int, C.c_int, C.c_void_p,
+                                                        C.c_size_t, C.c_void_p]
+        lib.fav4_bshd_forward_splitkv_paged.restype = C.c_int
+        lib.fav4_bshd_splitkv_paged_workspace_size.argtypes = [C.POINTER(PagedArgs), C.c_int, C.c_int]
+        lib.fav4_bshd_splitkv_paged_workspace_size.restype = C.c_longlong
+        lib.fav4_bshd_splitkv_paged_select.argtypes = [C.POINTER(PagedArgs), C.c_int]
+        lib.fav4_bshd_splitkv_paged_select.restype = C.c_int
         _LIB = lib
     return _LIB
 
@@ -281,6 +296,67 @@ class Runner:
                                                             workspace.data_ptr(), nbytes, stream)
         if status:
             raise RuntimeError(f"splitkv varlen splits {splits}: HIP status {status}")
+        return workspace
+
+
+    # ---- split-KV decode over paged K/V caches (no reference counterpart) ----
+    def paged_args(self, q, k_cache, v_cache, o, lse, cu_q, seqlens_k, block_table, max_q, max_k, total_k=None,
+                   scale=None) -> PagedArgs:
+        """q/o: [total_q, heads, 128]; k_cache/v_cache: [num_pages, page_size, kv_heads, 128] (BF16,
+        contiguous); cu_q: int32 [batch+1]; seqlens_k: int32 [batch]; block_table: int32
+        [batch, max_pages_per_seq] (device tensors); lse: FP32 [heads, total_q] or None.  total_k
+        (cached keys over the batch) only steers Auto; None passes max_k * batch."""
+        import torch
+        assert all(x.dtype == torch.bfloat16 and x.is_cuda and x.is_contiguous() for x in (q, k_cache, v_cache, o))
+        assert q.dim() == 3 and q.shape[2] == D and o.shape == q.shape
+        assert k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.shape[3] == D
+        assert all(c.dtype == torch.int32 and c.is_cuda and c.is_contiguous() for c in (cu_q, seqlens_k, block_table))
+        assert block_table.dim() == 2 and cu_q.numel() == seqlens_k.numel() + 1 == block_table.shape[0] + 1
+        tq, h, _ = q.shape
+        assert lse is None or (tuple(lse.shape) == (h, tq) and lse.is_contiguous() and lse.dtype == torch.float32)
+        b = seqlens_k.numel()
+        return PagedArgs(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), o.data_ptr(),
+                         lse.data_ptr() if lse is not None else None, cu_q.data_ptr(), seqlens_k.data_ptr(),
+                         block_table.data_ptr(), b, h, k_cache.shape[2], int(max_q), int(max_k), tq,
+                         int(max_k) * b if total_k is None else int(total_k), k_cache.shape[0], k_cache.shape[1],
+                         block_table.shape[1], 1 / math.sqrt(D) if scale is None else scale)
+
+    @staticmethod
+    def paged_shape_args(batch, heads, kv_heads, max_q, max_k, total_q, total_k, page_size, max_pages,
+                         num_pages) -> PagedArgs:
+        """Shape-only arguments for the select / workspace queries (no buffers)."""
+        return PagedArgs(None, None, None, None, None, None, None, None, batch, heads, kv_heads, max_q, max_k, total_q,
+                         total_k, num_pages, page_size, max_pages, 1 / math.sqrt(D))
+
+    def splitkv_paged_select(self, batch, heads, kv_heads, max_q, max_k, total_q, total_k, page_size, max_pages,
+                             num_pages) -> int:
+        a = self.paged_shape_args(batch, heads, kv_heads, max_q, max_k, total_q, total_k, page_size, max_pages,
+                                  num_pages)
+        return self.hip.fav4_bshd_splitkv_paged_select(C.byref(a), 0)
+
+    def splitkv_paged_workspace_size(self, batch, heads, kv_heads, max_q, max_k, total_q, total_k, page_size,
+                                     max_pages, num_pages, splits=0) -> int:
+        a = self.paged_shape_args(batch, heads, kv_heads, max_q, max_k, total_q, total_k, page_size, max_pages,
+                                  num_pages)
+        return self.hip.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), 0, int(splits))
+
+    def call_splitkv_paged(self, q, k_cache, v_cache, o, lse, cu_q, seqlens_k, block_table, max_q, max_k,
+                           splits=0, workspace=None, total_k=None, scale=None, stream=None):
+        """Dense decode over paged caches; `workspace` as for call_splitkv (None: allocated here)."""
+        import torch
+        a = self.paged_args(q, k_cache, v_cache, o, lse, cu_q, seqlens_k, block_table, max_q, max_k, total_k, scale)
+        if workspace is None:
+            need = self.hip.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), 0, int(splits))
+            if need < 0:
+                raise RuntimeError(f"splitkv paged splits {splits}: arguments rejected")
+            workspace = torch.empty(max(need, 1), device=q.device, dtype=torch.uint8)
+        nbytes = workspace.numel() * workspace.element_size()
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
+        status = self.hip.fav4_bshd_forward_splitkv_paged(C.byref(a), 0, int(splits), workspace.data_ptr(), nbytes,
+                                                           stream)
+        if status:
+            raise RuntimeError(f"splitkv paged splits {splits}: HIP status {status}")
         return workspace
 
 

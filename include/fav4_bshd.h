@@ -156,6 +156,53 @@ extern "C" int fav4_bshd_forward_splitkv_varlen(const Fav4VarlenArgs* args, int 
 extern "C" long long fav4_bshd_splitkv_varlen_workspace_size(const Fav4VarlenArgs* args, int causal, int splits);
 extern "C" int fav4_bshd_splitkv_varlen_select(const Fav4VarlenArgs* args, int causal);
 
+// ---- Paged K/V caches (decode) ------------------------------------------------
+// No counterpart in the reference.  The decode step over paged K/V caches:
+// packed sequences of 1-32 new queries (Q/O/LSE as in Fav4VarlenArgs), each
+// with its own number of cached keys, stored in fixed-size pages.  Key j of
+// sequence b is row block_table[b * max_pages_per_seq + j / page_size] *
+// page_size + j % page_size of the caches.  Dense only: causal must be 0 (a
+// top-left causal decode row would see only the first keys of its cache).
+// Runs the packed split-KV kernels (query heads of a K/V head share 32-row
+// tiles; chunks of a common number of key tiles, merged by log-sum-exp), so
+// per row the result is bitwise that of fav4_bshd_forward_splitkv_varlen on
+// the same keys stored contiguously, at the same chunk count.
+struct Fav4PagedArgs {
+    const void *q;                     // BF16 [total_q, heads, 128], contiguous
+    const void *k_cache, *v_cache;     // BF16 [num_pages, page_size, kv_heads, 128], contiguous
+    void *o;                           // BF16 [total_q, heads, 128], contiguous
+    float *lse;                        // optional FP32 [heads, total_q]; NULL = not written
+    const int *cu_seqlens_q;           // device int32 [batch + 1], non-decreasing from 0
+    const int *seqlens_k;              // device int32 [batch]: cached keys per sequence
+    const int *block_table;            // device int32 [batch, max_pages_per_seq]: page numbers
+    int batch, heads, kv_heads;        // kv_heads divides heads
+    int max_seqlen_q, max_seqlen_k;    // bounds of every sequence's query / key count
+    int total_q, total_k;              // rows of Q/O; cached keys over the batch (Auto only)
+    int num_pages, page_size, max_pages_per_seq;
+    float scale;
+};
+// Checks (before any HIP call; hipErrorInvalidValue otherwise): the pointers,
+// sizes >= 1 (total_k >= 0), kv_heads dividing heads, causal = 0, a finite
+// positive scale, max_seqlen_q <= 32, page_size a multiple of 32, max_seqlen_k
+// <= max_pages_per_seq * page_size and <= 2^19 (a chunk spans at most 64 key
+// tiles), page_size * kv_heads * 256 < 2^32, (heads / kv_heads) * max_seqlen_q
+// < 2^23, 16-byte aligned Q/O/caches and 4-byte aligned int arrays and LSE.
+// Device-read values are clamped (query offsets to [0, total_q], key counts to
+// [0, max_seqlen_k], page numbers to [0, num_pages)), so malformed tables give
+// undefined results but no access outside the buffers.  A sequence with no
+// keys gets O = 0 and LSE = -inf; one with no queries writes nothing.
+//  * splits: 0 = the Auto count of fav4_bshd_forward_splitkv_varlen on these
+//    sizes, else 1..256; either is raised if needed so that no chunk spans
+//    more than 64 key tiles.  One chunk still runs the split kernels.
+//  * workspace as for fav4_bshd_forward_splitkv, of
+//    fav4_bshd_splitkv_paged_workspace_size() bytes (never 0).
+// The two queries read only the sizes (pointers may be NULL) and return -1
+// for rejected arguments.
+extern "C" int fav4_bshd_forward_splitkv_paged(const Fav4PagedArgs* args, int causal, int splits,
+                                               void* workspace, size_t workspace_bytes, hipStream_t stream);
+extern "C" long long fav4_bshd_splitkv_paged_workspace_size(const Fav4PagedArgs* args, int causal, int splits);
+extern "C" int fav4_bshd_splitkv_paged_select(const Fav4PagedArgs* args, int causal);
+
 // ---- Arbitrary strides -----------------------------------------------------
 // No counterpart in the reference.  Q / O are read as [B, Sq, H, 128] and K /
 // V as [B, Sk, kv_heads, 128] views with the element (BF16) strides given per

@@ -50,7 +50,8 @@ def test_exports_exactly_the_c_abi():
                       "fav4_bshd_forward_varlen", "fav4_bshd_forward_strided", "fav4_bshd_forward_splitkv_gqa",
                       "fav4_bshd_splitkv_gqa_workspace_size", "fav4_bshd_splitkv_gqa_select",
                       "fav4_bshd_forward_splitkv_varlen", "fav4_bshd_splitkv_varlen_workspace_size",
-                      "fav4_bshd_splitkv_varlen_select"}, public
+                      "fav4_bshd_splitkv_varlen_select", "fav4_bshd_forward_splitkv_paged",
+                      "fav4_bshd_splitkv_paged_workspace_size", "fav4_bshd_splitkv_paged_select"}, public
 
 
 def test_ctypes_layout_matches_reference(Args):
@@ -445,6 +446,103 @@ def test_splitkv_varlen_rejects_workspace(lib, ws, nbytes):
     f.update(max_seqlen_q=1, max_seqlen_k=8192, total_q=3, total_k=9000)
     a = VarlenArgs(**f)
     assert lib.fav4_bshd_forward_splitkv_varlen(C.byref(a), 0, 8, ws, nbytes, None) == HIP_ERROR_INVALID_VALUE
+
+
+# ---- split-KV decode over paged K/V caches -------------------------------------
+PLAYOUT = dict(q=0, k_cache=8, v_cache=16, o=24, lse=32, cu_seqlens_q=40, seqlens_k=48, block_table=56, batch=64,
+               heads=68, kv_heads=72, max_seqlen_q=76, max_seqlen_k=80, total_q=84, total_k=88, num_pages=92,
+               page_size=96, max_pages_per_seq=100, scale=104)
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_paged_layout_ctypes_and_header(tmp_path):
+    PagedArgs = load_package().PagedArgs
+    assert C.sizeof(PagedArgs) == 112
+    for name, offset in PLAYOUT.items():
+        assert getattr(PagedArgs, name).offset == offset, name
+    src = tmp_path / "playout.cpp"
+    fields = ", ".join(f'offsetof(Fav4PagedArgs, {n})' for n in PLAYOUT)
+    src.write_text(
+        '#include <cstddef>\n#include <cstdio>\n#include "fav4_bshd.h"\n'
+        'int main() { size_t o[] = {' + fields + '};\n'
+        '  std::printf("%zu", sizeof(Fav4PagedArgs)); for (size_t x : o) std::printf(" %zu", x); }\n')
+    exe = tmp_path / "playout"
+    subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", f"-I{HEADER.parent}", "-I/opt/rocm/include",
+                    str(src), "-o", str(exe)], check=True, capture_output=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got == [112] + list(PLAYOUT.values())
+
+
+def _pgood(**kw):
+    f = dict(q=0x10000, k_cache=0x20000, v_cache=0x30000, o=0x40000, lse=None, cu_seqlens_q=0x50000,
+             seqlens_k=0x60000, block_table=0x70000, batch=3, heads=8, kv_heads=2, max_seqlen_q=4,
+             max_seqlen_k=5000, total_q=12, total_k=9000, num_pages=400, page_size=64, max_pages_per_seq=80,
+             scale=1 / math.sqrt(128))
+    f.update(kw)
+    return load_package().PagedArgs(**f)
+
+
+def _paged_plan(b, h, kvh, mq, mk, tk, splits):
+    """The packed-batch plan at these sizes with chunks capped at 64 key tiles."""
+    n, tps = _varlen_split_plan(b, h, kvh, mq, mk, tk, splits)
+    if tps > 64:
+        tps = 64
+        n = -(-(-(-mk // 32)) // 64)
+    return n, tps
+
+
+@pytest.mark.parametrize("shape", [(8, 32, 8, 1, 32768, 8 * 4096), (1, 8, 8, 1, 65536, 65536), (3, 8, 2, 4, 5000, 9000),
+                                   (16, 32, 4, 16, 2048, 16 * 1000), (1, 1, 1, 1, 524288, 524288),
+                                   (2, 4, 4, 32, 100, 3)])
+def test_splitkv_paged_plan(lib, shape):
+    b, h, kvh, mq, mk, tk = shape
+    a = _pgood(batch=b, heads=h, kv_heads=kvh, max_seqlen_q=mq, max_seqlen_k=mk, total_k=tk, total_q=b * mq,
+               page_size=32, max_pages_per_seq=-(-mk // 32), q=None, k_cache=None, v_cache=None, o=None,
+               cu_seqlens_q=None, seqlens_k=None, block_table=None)
+    n, tps = _paged_plan(b, h, kvh, mq, mk, tk, 0)
+    assert tps <= 64
+    assert lib.fav4_bshd_splitkv_paged_select(C.byref(a), 0) == n
+    assert lib.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), 0, 0) == n * b * h * mq * (128 * 4 + 8)
+    for req in (1, 3, 256):
+        n, tps = _paged_plan(b, h, kvh, mq, mk, tk, req)
+        assert tps <= 64
+        assert lib.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), 0, req) == n * b * h * mq * (128 * 4 + 8)
+
+
+PBAD = [("q_null", dict(q=None)), ("k_null", dict(k_cache=None)), ("v_null", dict(v_cache=None)),
+        ("o_null", dict(o=None)), ("cuq_null", dict(cu_seqlens_q=None)), ("seqk_null", dict(seqlens_k=None)),
+        ("table_null", dict(block_table=None)), ("batch0", dict(batch=0)), ("heads0", dict(heads=0)),
+        ("kv3", dict(kv_heads=3)), ("maxq0", dict(max_seqlen_q=0)), ("maxq33", dict(max_seqlen_q=33)),
+        ("maxk0", dict(max_seqlen_k=0)), ("totq0", dict(total_q=0)), ("totk_neg", dict(total_k=-1)),
+        ("pages0", dict(num_pages=0)), ("page16", dict(page_size=16)), ("page48", dict(page_size=48)),
+        ("maxpages0", dict(max_pages_per_seq=0)), ("table_short", dict(max_pages_per_seq=78)),
+        ("keys_2p19", dict(max_seqlen_k=524289, max_pages_per_seq=9000)),
+        ("page_huge", dict(page_size=1 << 21, kv_heads=8, max_pages_per_seq=1)),
+        ("group_rows", dict(heads=1 << 18, kv_heads=1, max_seqlen_q=32)),
+        ("scale0", dict(scale=0.0)), ("scale_nan", dict(scale=float("nan"))),
+        ("q_misaligned", dict(q=0x10008)), ("k_misaligned", dict(k_cache=0x20004)),
+        ("table_misaligned", dict(block_table=0x70002)), ("lse_misaligned", dict(lse=0x80001))]
+
+
+@pytest.mark.parametrize("name,change", PBAD, ids=[b[0] for b in PBAD])
+def test_splitkv_paged_rejects_bad_arguments(lib, name, change):
+    a = _pgood(**change)
+    assert lib.fav4_bshd_forward_splitkv_paged(C.byref(a), 0, 4, 0x100000, 1 << 40, None) == HIP_ERROR_INVALID_VALUE
+
+
+def test_splitkv_paged_rejects_causal_splits_and_workspace(lib):
+    a = _pgood()
+    assert lib.fav4_bshd_forward_splitkv_paged(C.byref(a), 1, 4, 0x100000, 1 << 40, None) == HIP_ERROR_INVALID_VALUE
+    for splits in (-1, 257):
+        assert lib.fav4_bshd_forward_splitkv_paged(C.byref(a), 0, splits, 0x100000, 1 << 40, None) == \
+            HIP_ERROR_INVALID_VALUE
+        assert lib.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), 0, splits) == -1
+    for ws, nbytes in ((None, 1 << 30), (0x100010, 1 << 30), (0x100000, 1000)):
+        assert lib.fav4_bshd_forward_splitkv_paged(C.byref(a), 0, 4, ws, nbytes, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_forward_splitkv_paged(None, 0, 4, 0x100000, 1 << 40, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_splitkv_paged_select(None, 0) == -1
+    assert lib.fav4_bshd_splitkv_paged_select(C.byref(a), 1) == -1
+    assert lib.fav4_bshd_splitkv_paged_workspace_size(None, 0, 0) == -1
 
 
 # ---- arbitrary strides -------------------------------------------------------

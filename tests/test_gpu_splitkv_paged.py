@@ -1,0 +1,152 @@
+"""GPU checks of split-KV decode over paged K/V caches (fav4_bshd_forward_splitkv_paged) via the C ABI.
+
+Each sequence's keys are scattered over randomly chosen pages of the caches;
+the pages no sequence uses hold NaN, and block-table entries past a
+sequence's pages hold out-of-range numbers (which the kernel clamps and never
+reads through), so a wrong page, slot or head shows up.  Pins:
+  * bitwise equality with fav4_bshd_forward_splitkv_varlen on the same keys
+    stored contiguously, at the same explicit chunk count (same plan, chunk
+    bounds and merge), for page sizes 32, 64 and 256 and MHA / GQA / MQA;
+  * every sequence against the FP64 oracle at the reference harness's bar,
+    Auto and explicit chunk counts, LSE on and off;
+  * a sequence without queries writes nothing, one without keys gets O = 0
+    and LSE = -inf, and rows after O / LSE are never written.
+"""
+import numpy as np
+import pytest
+
+from oracle import attention as orc
+from tests.conftest import to_device, to_host_bits
+
+pytestmark = pytest.mark.gpu
+
+GUARD = 64
+NAN_BF16 = 0x7FC0
+
+# (heads, kv_heads, page_size, [(sq, sk), ...], explicit chunk count)
+CASES = [
+    (32, 8, 32, [(1, 4096), (1, 100), (1, 1), (1, 9000), (1, 33), (1, 2048)], 7),
+    (8, 1, 64, [(16, 3000), (5, 1), (32, 700), (1, 5000)], 5),
+    (4, 4, 256, [(3, 300), (32, 4096), (0, 50), (7, 0), (1, 20000)], 16),
+    (6, 2, 32, [(32, 32), (31, 64), (17, 1025)], 2),
+]
+
+
+def _build(heads, kv_heads, page_size, lens, seed):
+    """Packed Q, contiguous packed K/V, and paged caches holding the same keys."""
+    rng = np.random.default_rng(seed)
+    qs, ks, vs = [], [], []
+    for i, (sq, sk) in enumerate(lens):
+        q, _, _ = orc.make_inputs(1, heads, max(sq, 1), max(sk, 1), "normal", seed=seed + 2 * i)
+        _, k, v = orc.make_inputs(1, kv_heads, max(sq, 1), max(sk, 1), "normal", seed=seed + 2 * i + 1)
+        qs.append(q[0, :sq])
+        ks.append(k[0, :sk])
+        vs.append(v[0, :sk])
+    npages = [-(-sk // page_size) for _, sk in lens]
+    max_pages = max(max(npages), 1)
+    num_pages = sum(npages) + 7                       # 7 pages nobody uses
+    perm = rng.permutation(num_pages)
+    kc = np.full((num_pages, page_size, kv_heads, 128), NAN_BF16, dtype=np.uint16)
+    vc = np.full_like(kc, NAN_BF16)
+    table = rng.choice([-3, num_pages, 1 << 30], size=(len(lens), max_pages)).astype(np.int32)
+    nxt = 0
+    for i, (_, sk) in enumerate(lens):
+        for p in range(npages[i]):
+            page = perm[nxt]
+            nxt += 1
+            table[i, p] = page
+            rows = slice(p * page_size, min(sk, (p + 1) * page_size))
+            n = rows.stop - rows.start
+            kc[page, :n] = ks[i][rows]
+            vc[page, :n] = vs[i][rows]
+    cu_q = np.concatenate([[0], np.cumsum([s for s, _ in lens])]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum([s for _, s in lens])]).astype(np.int32)
+    seqlens_k = np.array([s for _, s in lens], dtype=np.int32)
+    return (np.concatenate(qs), np.concatenate(ks), np.concatenate(vs), kc, vc, cu_q, cu_k, seqlens_k, table)
+
+
+def _out(torch, dev, tq, h, with_lse):
+    o_buf = torch.full((tq + GUARD, h, 128), float("nan"), device=dev, dtype=torch.bfloat16)
+    l_buf = torch.full((h * tq + GUARD,), float("nan"), device=dev, dtype=torch.float32)
+    return o_buf, l_buf, o_buf[:tq], (l_buf[:h * tq].view(h, tq) if with_lse else None)
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "h%dkv%d_p%d_n%d" % (c[0], c[1], c[2], len(c[3])))
+def test_splitkv_paged(gpu_runner, case):
+    import torch
+    h, kvh, ps, lens, splits = case
+    q, k, v, kc, vc, cu_q, cu_k, seqlens_k, table = _build(h, kvh, ps, lens, seed=17)
+    dev = torch.device("cuda:0")
+    qd, kd, vd, kcd, vcd = (to_device(x, dev) for x in (q, k, v, kc, vc))
+    cq, ck, sk_d, tb = (torch.from_numpy(x).to(dev) for x in (cu_q, cu_k, seqlens_k, table))
+    max_q = max(s for s, _ in lens)
+    max_k = max(s for _, s in lens)
+    tq, group = len(q), h // kvh
+    print(f"  splitkv paged H{h} KVH{kvh} page {ps} lens={lens} splits={splits}", flush=True)
+
+    # bitwise against the contiguous packed split-KV at the same chunk count
+    ob, lb, o, lse = _out(torch, dev, tq, h, True)
+    gpu_runner.call_splitkv_paged(qd, kcd, vcd, o, lse, cq, sk_d, tb, max_q, max_k, splits, total_k=len(k))
+    ob2, lb2, o2, lse2 = _out(torch, dev, tq, h, True)
+    gpu_runner.call_splitkv_varlen(qd, kd, vd, o2, lse2, cq, ck, max_q, max_k, False, splits)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), o2.view(torch.int16))
+    assert torch.equal(lse.view(torch.int32), lse2.view(torch.int32))
+    assert torch.isnan(ob[tq:]).all().item() and torch.isnan(lb[h * tq:]).all().item()
+
+    # Auto, LSE off, against the oracle (and the explicit run's empty rows)
+    ob3, lb3, o3, _ = _out(torch, dev, tq, h, False)
+    gpu_runner.call_splitkv_paged(qd, kcd, vcd, o3, None, cq, sk_d, tb, max_q, max_k, 0, total_k=len(k))
+    torch.cuda.synchronize()
+    assert torch.isnan(ob3[tq:]).all().item() and torch.isnan(lb3).all().item()
+    for i, (sq, sk) in enumerate(lens):
+        a, b = cu_q[i], cu_q[i + 1]
+        c, d = cu_k[i], cu_k[i + 1]
+        if sq == 0:
+            continue
+        if sk == 0:
+            assert (o[a:b].float() == 0).all().item() and (o3[a:b].float() == 0).all().item(), i
+            assert torch.isneginf(lse[:, a:b]).all().item(), i
+            continue
+        ke = np.repeat(k[c:d][None], group, axis=2)
+        ve = np.repeat(v[c:d][None], group, axis=2)
+        ref, ref_lse = orc.attention_fp64(q[a:b][None], ke, ve, orc.DEFAULT_SCALE, False)
+        e = orc.errors(to_host_bits(o[a:b])[None], lse[:, a:b].cpu().numpy()[None], ref, ref_lse)
+        assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (i, sq, sk, e)
+        e3 = orc.errors(to_host_bits(o3[a:b])[None], None, ref, None)
+        assert orc.check_acceptance_tolerance(e3) and orc.check_reference_tolerance(e3), ("auto", i, e3)
+
+
+def test_splitkv_paged_single_chunk_and_long_cache(gpu_runner):
+    """One chunk (max_seqlen_k <= 64 key tiles: still the split kernels and the
+    merge), and a cache long enough that the 64-tile chunk cap raises an
+    explicit count of 2 (2188 key tiles -> 35 chunks)."""
+    import torch
+    h, kvh, ps = 16, 4, 128
+    dev = torch.device("cuda:0")
+    group = h // kvh
+    for lens, max_k, splits, want in (([(2, 2048), (1, 700), (3, 0)], 2048, 1, 1),
+                                      ([(2, 70000), (1, 5000)], 70000, 2, 35)):
+        q, k, v, kc, vc, cu_q, cu_k, seqlens_k, table = _build(h, kvh, ps, lens, seed=23)
+        qd, kcd, vcd = (to_device(x, dev) for x in (q, kc, vc))
+        cq, sk_d, tb = (torch.from_numpy(x).to(dev) for x in (cu_q, seqlens_k, table))
+        max_q = max(s for s, _ in lens)
+        need = gpu_runner.splitkv_paged_workspace_size(len(lens), h, kvh, max_q, max_k, len(q), len(k), ps,
+                                                       table.shape[1], len(kc), splits)
+        assert need == want * len(lens) * h * max_q * 520, (lens, need)
+        print(f"  splitkv paged lens={lens} splits={splits} -> {want} chunks", flush=True)
+        ob, lb, o, lse = _out(torch, dev, len(q), h, True)
+        gpu_runner.call_splitkv_paged(qd, kcd, vcd, o, lse, cq, sk_d, tb, max_q, max_k, splits)
+        torch.cuda.synchronize()
+        assert torch.isnan(ob[len(q):]).all().item() and torch.isnan(lb[h * len(q):]).all().item()
+        for i, (sq, sk) in enumerate(lens):
+            a, b = cu_q[i], cu_q[i + 1]
+            c, d = cu_k[i], cu_k[i + 1]
+            if sk == 0:
+                assert (o[a:b].float() == 0).all().item() and torch.isneginf(lse[:, a:b]).all().item(), i
+                continue
+            ke = np.repeat(k[c:d][None], group, axis=2)
+            ve = np.repeat(v[c:d][None], group, axis=2)
+            ref, ref_lse = orc.attention_fp64(q[a:b][None], ke, ve, orc.DEFAULT_SCALE, False)
+            e = orc.errors(to_host_bits(o[a:b])[None], lse[:, a:b].cpu().numpy()[None], ref, ref_lse)
+            assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (splits, i, e)
