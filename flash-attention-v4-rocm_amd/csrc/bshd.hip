@@ -318,10 +318,15 @@ Fav4Args varlen_shape(const Fav4VarlenArgs& v) {
 // one chunk, the plain packed forward).  Chunks are a fixed number of key
 // tiles for every sequence, so a sequence has as many non-empty chunks as its
 // keys need.  Auto takes the chunk size of the contiguous-batch Auto plan at
-// the mean key length (total_k / batch), enlarged if the longest sequence
-// would need more than MAX_SPLITS chunks: a ragged batch's long sequences
-// thus spread over as many workgroups as a uniform batch's, and a uniform
-// batch gets exactly the contiguous plan.
+// the mean key length (total_k / batch), so a uniform batch gets exactly the
+// contiguous plan.  A ragged batch (mean below 3/4 of the longest) gets
+// chunks of at most RAGGED_TPS key tiles: its chunks differ in length, and
+// more, shorter ones even out the CUs' finishing times (measured on MI355X,
+// against the uncapped plan: +0.7%, +2% and +13% on three ragged batches;
+// the same cap on uniform batches lost 3-25%).  Either is enlarged if the
+// longest sequence would need more than MAX_SPLITS chunks.
+constexpr int RAGGED_TPS = 64;
+
 // `a` is the packed batch's shape (max lengths), total_k its key count.
 SplitPlan packed_split_plan(const Fav4Args& a, int kv_heads, int64_t total_k, int causal, int req) {
     if (a.sq > DECODE_SQ) return {1, 1, split_shape(a), 1, 1};
@@ -331,7 +336,9 @@ SplitPlan packed_split_plan(const Fav4Args& a, int kv_heads, int64_t total_k, in
         mean.sk = int(std::max<int64_t>(1, std::min<int64_t>(a.sk, (total_k + a.batch - 1) / a.batch)));
         const int keys = causal ? std::min(a.sk, a.sq) : a.sk;
         const int ktiles = (keys + p.shape.bn - 1) / p.shape.bn;
-        p.tps = std::max(split_plan(mean, kv_heads, causal, 0).tps, (ktiles + fav4::MAX_SPLITS - 1) / fav4::MAX_SPLITS);
+        int tps = split_plan(mean, kv_heads, causal, 0).tps;
+        if (4 * int64_t(mean.sk) < 3 * int64_t(a.sk)) tps = std::min(tps, RAGGED_TPS);
+        p.tps = std::max(tps, (ktiles + fav4::MAX_SPLITS - 1) / fav4::MAX_SPLITS);
         p.splits = (ktiles + p.tps - 1) / p.tps;
     }
     return p;

@@ -143,7 +143,8 @@ extern "C" int fav4_bshd_forward_varlen(const Fav4VarlenArgs* args, int causal, 
 // as fav4_bshd_forward_varlen (O and LSE rows, empty sequences, offset
 // clamping), plus:
 //  * splits: 0 = library choice (the chunk size the contiguous split-KV Auto
-//    plan gives at the mean key length total_k / batch, enlarged so that the
+//    plan gives at the mean key length total_k / batch, at most 64 key tiles
+//    when that mean is below 3/4 of max_seqlen_k, enlarged so that the
 //    longest sequence needs at most 256 chunks), else 1..256 chunks of the
 //    longest sequence (clamped to its key tiles);
 //  * workspace as for fav4_bshd_forward_splitkv, of

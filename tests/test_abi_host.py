@@ -368,15 +368,19 @@ def test_varlen_rejects_bad_causal(lib, causal):
 def _varlen_split_plan(batch, h, kvh, max_q, max_k, total_k, splits, causal=False, cus=256):
     """Closed form of the packed-batch plan: one chunk for max_q > 32; explicit
     counts as the contiguous plan at the max lengths; Auto takes the chunk size
-    (key tiles) of the contiguous Auto plan at the mean key length, enlarged to
-    keep the longest sequence within 256 chunks."""
+    (key tiles) of the contiguous Auto plan at the mean key length, at most 64
+    tiles when the mean is below 3/4 of the longest, enlarged to keep the
+    longest sequence within 256 chunks."""
     if max_q > 32:
         return 1, 1
     if splits:
         return _split_plan(batch, h, max_q, max_k, splits, causal=causal, kvh=kvh)
     mean = max(1, min(max_k, -(-total_k // batch)))
     ktiles = -(-(min(max_k, max_q) if causal else max_k) // 32)
-    tps = max(_split_plan(batch, h, max_q, mean, 0, cus=cus, causal=causal, kvh=kvh)[1], -(-ktiles // 256))
+    tps = _split_plan(batch, h, max_q, mean, 0, cus=cus, causal=causal, kvh=kvh)[1]
+    if 4 * mean < 3 * max_k:        # ragged: chunks of at most 64 key tiles
+        tps = min(tps, 64)
+    tps = max(tps, -(-ktiles // 256))
     return -(-ktiles // tps), tps
 
 
