@@ -54,7 +54,8 @@ extern "C" int fav4_bshd_select_config(const Fav4Args* args);
 // Same argument contract as fav4_bshd_forward (config is always Auto), plus:
 //  * splits: 0 = library choice (enough chunks to fill every CU once, >= 4
 //    key tiles per chunk, at most 64 chunks; for Sq <= 32 one-wave
-//    workgroups over 32-key tiles, three per CU, at most 128 chunks; for
+//    workgroups over 32-key tiles, three per CU, at most 128 chunks, 256
+//    when there are only one or two (batch, K/V head) tiles; for
 //    Sq > 32 then the count up to that one, 1 included, with the lowest
 //    time predicted by a cost model fitted on MI355X), else 1..256 (clamped
 //    to the key tiles);

@@ -158,6 +158,8 @@ def _split_plan(b, h, sq, sk, splits, cus=None, causal=False, kvh=None):
     ktiles = -(-(min(sk, sq) if causal else sk) // bn)
     if splits == 0:
         items = b * kvh * -(-(h // kvh) * sq // bm) if sq <= 32 else b * h * -(-sq // bm)
+        if sq <= 32 and items <= 2:     # one or two decode tiles: up to 256 chunks
+            amax = 256
         splits = min(-(-(cus * per_cu) // items), min(amax, max(1, ktiles // 4)))
         if sq > 32 and splits > 1:
             splits = _prefill_auto(b, h, sq, sk, causal, splits, ktiles, cus)
@@ -247,6 +249,8 @@ def test_splitkv_plan_examples():
     # MQA decode, 16 queries x 8 heads = 128 packed rows = 4 tiles per batch:
     # 96 chunks wanted over 512 key tiles -> 86 of 6
     assert _split_plan(2, 8, 16, 16384, 0, cus=256, kvh=1) == (86, 6)
+    # one decode tile (B1 MQA, 6250 key tiles): 256 chunks of 25 tiles
+    assert _split_plan(1, 8, 1, 200000, 0, cus=256, kvh=1) == (250, 25)
 
 
 @pytest.mark.parametrize("shape", [(4, 32, 8, 1, 32768), (2, 8, 1, 16, 16384), (1, 12, 3, 5, 4000),
