@@ -150,3 +150,64 @@ def test_splitkv_paged_single_chunk_and_long_cache(gpu_runner):
             ref, ref_lse = orc.attention_fp64(q[a:b][None], ke, ve, orc.DEFAULT_SCALE, False)
             e = orc.errors(to_host_bits(o[a:b])[None], lse[:, a:b].cpu().numpy()[None], ref, ref_lse)
             assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (splits, i, e)
+
+
+def _draw(rng):
+    kvh = int(rng.choice([1, 2, 4]))
+    group = int(rng.choice([1, 2, 4, 8]))
+    b = int(rng.integers(1, 7))
+    sq_max = int(rng.choice([1, 4, 32]))
+    lens = [(int(rng.integers(0, sq_max + 1)), int(rng.integers(0, 6000))) for _ in range(b)]
+    lens[0] = (max(lens[0][0], 1), max(lens[0][1], 40))        # at least one row with keys past one tile
+    return dict(h=kvh * group, kvh=kvh, ps=int(rng.choice([32, 64, 128, 512])), lens=lens,
+                splits=int(rng.choice([2, 3, 8, 33, 200])), lse=bool(rng.integers(0, 2)))
+
+
+RANDOM = [_draw(np.random.default_rng(500 + i)) for i in range(12)]
+
+
+@pytest.mark.parametrize("case", RANDOM, ids=lambda c: "h%dkv%d_p%d_b%d_s%d" % (c["h"], c["kvh"], c["ps"],
+                                                                                len(c["lens"]), c["splits"]))
+def test_splitkv_paged_random(gpu_runner, case):
+    """Seeded random batches: bitwise the contiguous packed split-KV at the same
+    explicit chunk count, and the FP64 oracle on every sequence."""
+    import torch
+    h, kvh, ps, lens, splits, with_lse = case["h"], case["kvh"], case["ps"], case["lens"], case["splits"], case["lse"]
+    q, k, v, kc, vc, cu_q, cu_k, seqlens_k, table = _build(h, kvh, ps, lens, seed=31)
+    dev = torch.device("cuda:0")
+    qd, kd, vd, kcd, vcd = (to_device(x, dev) for x in (q, k, v, kc, vc))
+    cq, ck, sk_d, tb = (torch.from_numpy(x).to(dev) for x in (cu_q, cu_k, seqlens_k, table))
+    max_q = max(s for s, _ in lens)
+    max_k = max(s for _, s in lens)
+    tq, group = len(q), h // kvh
+    print(f"  splitkv paged random H{h} KVH{kvh} page {ps} lens={lens} splits={splits}", flush=True)
+    ob, lb, o, lse = _out(torch, dev, tq, h, with_lse)
+    gpu_runner.call_splitkv_paged(qd, kcd, vcd, o, lse, cq, sk_d, tb, max_q, max_k, splits, total_k=len(k))
+    torch.cuda.synchronize()
+    assert torch.isnan(ob[tq:]).all().item() and torch.isnan(lb[h * tq:]).all().item()
+    # Same plan (the paged one caps chunks at 64 key tiles, which only ever
+    # raises the count): same workspace size.
+    ws_v = gpu_runner.splitkv_varlen_workspace_size(len(lens), h, kvh, max_q, max_k, tq, len(k), False, splits)
+    ws_p = gpu_runner.splitkv_paged_workspace_size(len(lens), h, kvh, max_q, max_k, tq, len(k), ps, table.shape[1],
+                                                   len(kc), splits)
+    if ws_v == ws_p:
+        _, _, o2, lse2 = _out(torch, dev, tq, h, with_lse)
+        gpu_runner.call_splitkv_varlen(qd, kd, vd, o2, lse2, cq, ck, max_q, max_k, False, splits)
+        torch.cuda.synchronize()
+        assert torch.equal(o.view(torch.int16), o2.view(torch.int16))
+        if with_lse:
+            assert torch.equal(lse.view(torch.int32), lse2.view(torch.int32))
+    for i, (sq, sk) in enumerate(lens):
+        a, b = cu_q[i], cu_q[i + 1]
+        c, d = cu_k[i], cu_k[i + 1]
+        if sq == 0:
+            continue
+        if sk == 0:
+            assert (o[a:b].float() == 0).all().item(), i
+            continue
+        ke = np.repeat(k[c:d][None], group, axis=2)
+        ve = np.repeat(v[c:d][None], group, axis=2)
+        ref, ref_lse = orc.attention_fp64(q[a:b][None], ke, ve, orc.DEFAULT_SCALE, False)
+        got_lse = lse[:, a:b].cpu().numpy()[None] if with_lse else None
+        e = orc.errors(to_host_bits(o[a:b])[None], got_lse, ref, ref_lse if with_lse else None)
+        assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (i, sq, sk, e)
