@@ -227,16 +227,20 @@ int split_args_ok(const Fav4Args* a, int kv_heads, int causal, int splits) {
 // sequence offsets; decode shape only.  PAGED: the same over paged K/V caches.
 // Top-left causal decode (sq <= 32) sees at most 32 keys, one tile, so the
 // plan never splits it: causal launches use the prefill shape only.
-template <bool CAUSAL, bool VARLEN = false, bool PAGED = false>
+// BR (packed decode only): bottom-right causal, the one causal mask a decode
+// splits.
+template <bool CAUSAL, bool VARLEN = false, bool PAGED = false, bool BR = false>
 int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, fav4::SplitArgs sp,
                  hipStream_t stream) {
-    static_assert(!(CAUSAL && VARLEN), "causal decode never splits");
+    static_assert(!(CAUSAL && VARLEN) || BR, "top-left causal decode never splits");
+    static_assert(!BR || (CAUSAL && VARLEN), "bottom-right causal is for packed decode");
     static_assert(!PAGED || VARLEN, "paged caches hold packed sequences");
     const int tiles = p.tiles;
     const int64_t total = p.items * tiles * p.splits;
     const int64_t rows = int64_t(a.batch) * a.heads * a.sq;
     const bool decode = p.shape.bm == 32;
-    if (total > INT_MAX || rows > INT_MAX || (VARLEN && !decode) || (CAUSAL && decode)) return hipErrorInvalidValue;
+    if (total > INT_MAX || rows > INT_MAX || (VARLEN && !decode) || (CAUSAL && !BR && decode))
+        return hipErrorInvalidValue;
     sp.o_part = static_cast<float*>(ws);
     sp.lse_part = sp.o_part + int64_t(p.splits) * rows * fav4::D;
     sp.splits = p.splits;
@@ -247,8 +251,8 @@ int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, 
         hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, stream, a, sp, kv_heads, tiles, int(total));
     };
     if constexpr (VARLEN) {
-        if (a.lse) go(fav4::fwd_kernel_split<32, false, 1, true, true, PAGED>, 64);
-        else go(fav4::fwd_kernel_split<32, false, 1, false, true, PAGED>, 64);
+        if (a.lse) go(fav4::fwd_kernel_split<32, BR, 1, true, true, PAGED, BR>, 64);
+        else go(fav4::fwd_kernel_split<32, BR, 1, false, true, PAGED, BR>, 64);
     } else if constexpr (CAUSAL) {
         if (a.lse) go(fav4::fwd_kernel_split<64, true, 8, true>, 512);
         else go(fav4::fwd_kernel_split<64, true, 8, false>, 512);
@@ -349,17 +353,30 @@ SplitPlan packed_split_plan(const Fav4Args& a, int kv_heads, int64_t total_k, in
     return p;
 }
 
+// causal = 2 in the packed decode calls: bottom-right causal (query i of a
+// sequence with sq queries and sk keys sees keys j <= sk - sq + i).  It sees
+// as many keys as a dense call, so it is planned like one, and it always runs
+// the split kernels (the unsplit packed forward has no such mask).
+constexpr int BOTTOM_RIGHT = 2;
+
 SplitPlan varlen_split_plan(const Fav4VarlenArgs& v, int causal, int req) {
-    return packed_split_plan(varlen_shape(v), v.kv_heads, v.total_k, causal, req);
+    return packed_split_plan(varlen_shape(v), v.kv_heads, v.total_k, causal == BOTTOM_RIGHT ? 0 : causal, req);
 }
 
 int varlen_split_ok(const Fav4VarlenArgs* v, int causal, int splits, bool buffers) {
-    const int st = buffers ? varlen_ok(v, causal) : varlen_shape_ok(v, causal);
+    const bool br = causal == BOTTOM_RIGHT;
+    const int st = buffers ? varlen_ok(v, br ? 0 : causal) : varlen_shape_ok(v, br ? 0 : causal);
     if (st != hipSuccess) return st;
     if (splits < 0 || splits > fav4::MAX_SPLITS) return hipErrorInvalidValue;
-    if (v->max_seqlen_q > DECODE_SQ) return hipSuccess;
+    if (v->max_seqlen_q > DECODE_SQ) return br ? hipErrorInvalidValue : hipSuccess;
     const Fav4Args a = varlen_shape(*v);
-    return split_shape_ok(&a, v->kv_heads, causal, splits);
+    return split_shape_ok(&a, v->kv_heads, br ? 0 : causal, splits);
+}
+
+// Workspace of a packed plan; bottom-right causal needs it for one chunk too.
+int64_t varlen_workspace(const Fav4VarlenArgs& v, const SplitPlan& p, int causal) {
+    if (p.splits <= 1 && causal != BOTTOM_RIGHT) return 0;
+    return int64_t(p.splits) * v.batch * v.heads * v.max_seqlen_q * (fav4::D * 4 + 2 * 4);
 }
 
 // ---- paged K/V caches ----------------------------------------------------
@@ -370,7 +387,8 @@ int paged_shape_ok(const Fav4PagedArgs* a, int causal, int splits) {
     if (!a || a->batch <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads != 0 ||
         a->max_seqlen_q <= 0 || a->max_seqlen_q > DECODE_SQ || a->max_seqlen_k <= 0 || a->total_q <= 0 ||
         a->total_k < 0 || a->num_pages <= 0 || a->page_size <= 0 || a->page_size % 32 != 0 ||
-        a->max_pages_per_seq <= 0 || causal != 0 || !std::isfinite(a->scale) || a->scale <= 0 || splits < 0 ||
+        a->max_pages_per_seq <= 0 || (causal != 0 && causal != BOTTOM_RIGHT) || !std::isfinite(a->scale) ||
+        a->scale <= 0 || splits < 0 ||
         splits > fav4::MAX_SPLITS)
         return hipErrorInvalidValue;
     if (a->batch > INT_MAX - 1 || a->heads > INT_MAX / 256 || a->max_seqlen_k > PAGED_MAX_KEYS ||
@@ -570,7 +588,7 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_splitkv_varlen_s
 extern "C" __attribute__((visibility("default"))) long long fav4_bshd_splitkv_varlen_workspace_size(
     const Fav4VarlenArgs* a, int causal, int splits) {
     if (varlen_split_ok(a, causal, splits, false) != hipSuccess) return -1;
-    return split_workspace(varlen_shape(*a), varlen_split_plan(*a, causal, splits));
+    return varlen_workspace(*a, varlen_split_plan(*a, causal, splits), causal);
 }
 
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_varlen(const Fav4VarlenArgs* a,
@@ -583,9 +601,10 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_
     const SplitPlan p = varlen_split_plan(*a, causal, splits);
     // Top-left causal decode (max_seqlen_q <= 32) sees at most 32 keys, one
     // tile: the plan never splits it.
-    if (p.splits == 1 || causal) return fav4_bshd_forward_varlen(a, causal, stream);
+    const bool br = causal == BOTTOM_RIGHT;
+    if (!br && (p.splits == 1 || causal)) return fav4_bshd_forward_varlen(a, causal, stream);
     const Fav4Args shape = varlen_shape(*a);
-    const int64_t need = split_workspace(shape, p);
+    const int64_t need = varlen_workspace(*a, p, causal);
     if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || uint64_t(need) > workspace_bytes)
         return hipErrorInvalidValue;
     fav4::SplitArgs sp{};
@@ -593,7 +612,8 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_
     sp.cu_k = a->cu_seqlens_k;
     sp.total_q = a->total_q;
     sp.total_k = a->total_k;
-    return launch_split<false, true>(shape, a->kv_heads, p, workspace, sp, stream);
+    return br ? launch_split<true, true, false, true>(shape, a->kv_heads, p, workspace, sp, stream)
+              : launch_split<false, true>(shape, a->kv_heads, p, workspace, sp, stream);
 }
 
 // Split-KV decode over paged K/V caches (no counterpart in the reference).
@@ -628,5 +648,7 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_
     sp.page_size = a->page_size;
     sp.max_pages = a->max_pages_per_seq;
     sp.num_pages = a->num_pages;
-    return launch_split<false, true, true>(paged_shape(*a), a->kv_heads, p, workspace, sp, stream);
+    return causal == BOTTOM_RIGHT
+               ? launch_split<true, true, true, true>(paged_shape(*a), a->kv_heads, p, workspace, sp, stream)
+               : launch_split<false, true, true>(paged_shape(*a), a->kv_heads, p, workspace, sp, stream);
 }

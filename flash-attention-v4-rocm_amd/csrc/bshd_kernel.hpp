@@ -626,16 +626,20 @@ __device__ __forceinline__ SeqSpan seq_span(const SplitArgs& sp, int b, int max_
 // PAGED (with VARLEN): K/V come from paged caches.  page_size is a multiple
 // of BN, so a key tile lies in one page; a chunk spans at most 64 pages, whose
 // (clamped) numbers one load puts in the wave's lanes at the chunk start.
+// BR (with CAUSAL, one wave): bottom-right causal, query i of a sequence with
+// sq queries and sk keys sees keys j <= sk - sq + i (the last query sees all
+// of them; with sq > sk the first sq - sk rows see none).
 // The one-wave shape keeps the 8-wave shape's 256-register budget
 // (waves_per_eu 2); its occupancy is set by LDS (three workgroups per CU), so
 // the compiler's note that it cannot reach two waves per SIMD is expected.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Wpass-failed"
-template <int BN, bool CAUSAL, int WAVES, bool LSE, bool VARLEN = false, bool PAGED = false>
+template <int BN, bool CAUSAL, int WAVES, bool LSE, bool VARLEN = false, bool PAGED = false, bool BR = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int total) {
     static_assert(!VARLEN || WAVES == 1, "packed sequences use the one-wave shape");
     static_assert(!PAGED || VARLEN, "paged caches hold packed sequences");
+    static_assert(!BR || (CAUSAL && WAVES == 1), "bottom-right causal is a decode mask");
     constexpr int BM = WAVES * 32, STAGES = 3;
     // One wave (decode): the q-tile rows are the group's query heads times
     // their sq queries, row r = (head - first head of the group) * sq + query,
@@ -724,10 +728,12 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
         const rsrc_t rp = make_rsrc(sp.o_part + prow0 * D, uint32_t(rows - q0) * D * 4);
         // PACK: every q tile holds rows of query 0 and of the last query, so
         // the causal range is the whole [0, min(sk, sq)) and no tile is
-        // unmasked for every row.
-        const int kend = CAUSAL ? min(sk, PACK ? sq : q0 + BM) : sk;
+        // unmasked for every row.  BR: the range is [0, sk), unmasked for
+        // every row below key sk - sq + 1 (query 0's first hidden key).
+        const int kend = CAUSAL && !BR ? min(sk, PACK ? sq : q0 + BM) : sk;
         const int ntiles = (kend + BN - 1) / BN;
-        const int nfull = (CAUSAL ? (PACK ? 0 : min(sk, q0 + 1)) : sk) / BN;
+        const int nfull = (BR ? max(0, sk - sq + 1) : CAUSAL ? (PACK ? 0 : min(sk, q0 + 1)) : sk) / BN;
+        const int climit = BR ? qi + sk - sq : qi;     // last visible key of this lane's row
         const int t0 = split * sp.tps, t1 = min(ntiles, t0 + sp.tps);
 
         RowState st;
@@ -790,7 +796,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
                 const unsigned char* cur = smem + STAGE * STAGE_BYTES;
                 sync_and_prefetch(t);
                 attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE, CAUSAL>(
-                    cur, cur + TILE_BYTES, off, qr, st, t == t0, t * BN, sk, qi, half, scale2);
+                    cur, cur + TILE_BYTES, off, qr, st, t == t0, t * BN, sk, climit, half, scale2);
             };
             using S0 = std::integral_constant<int, 0>;
             using S1 = std::integral_constant<int, 1>;

@@ -341,20 +341,21 @@ class Runner:
         return self.hip.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), 0, int(splits))
 
     def call_splitkv_paged(self, q, k_cache, v_cache, o, lse, cu_q, seqlens_k, block_table, max_q, max_k,
-                           splits=0, workspace=None, total_k=None, scale=None, stream=None):
-        """Dense decode over paged caches; `workspace` as for call_splitkv (None: allocated here)."""
+                           splits=0, workspace=None, total_k=None, scale=None, stream=None, causal=0):
+        """Decode over paged caches (causal 0 = dense, 2 = bottom-right); `workspace` as for
+        call_splitkv (None: allocated here)."""
         import torch
         a = self.paged_args(q, k_cache, v_cache, o, lse, cu_q, seqlens_k, block_table, max_q, max_k, total_k, scale)
         if workspace is None:
-            need = self.hip.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), 0, int(splits))
+            need = self.hip.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), int(causal), int(splits))
             if need < 0:
                 raise RuntimeError(f"splitkv paged splits {splits}: arguments rejected")
             workspace = torch.empty(max(need, 1), device=q.device, dtype=torch.uint8)
         nbytes = workspace.numel() * workspace.element_size()
         if stream is None:
             stream = torch.cuda.current_stream().cuda_stream
-        status = self.hip.fav4_bshd_forward_splitkv_paged(C.byref(a), 0, int(splits), workspace.data_ptr(), nbytes,
-                                                           stream)
+        status = self.hip.fav4_bshd_forward_splitkv_paged(C.byref(a), int(causal), int(splits), workspace.data_ptr(),
+                                                           nbytes, stream)
         if status:
             raise RuntimeError(f"splitkv paged splits {splits}: HIP status {status}")
         return workspace

@@ -140,7 +140,12 @@ extern "C" int fav4_bshd_forward_varlen(const Fav4VarlenArgs* args, int causal, 
 // with equal lengths the result is bitwise that call's on the same data at
 // the same chunk count.  Anything else (max_seqlen_q > 32, or causal = 1:
 // top-left causal decode sees at most 32 keys) takes one chunk, i.e. runs
-// fav4_bshd_forward_varlen, and needs no workspace.  Same argument contract
+// fav4_bshd_forward_varlen, and needs no workspace.
+// causal = 2 (these calls and the paged ones only; max_seqlen_q <= 32):
+// bottom-right causal, query i of a sequence with sq queries and sk keys sees
+// keys j <= sk - sq + i (the last query sees them all; with sq > sk the first
+// sq - sk rows see none: O = 0, LSE = -inf).  It is planned like a dense call
+// and always runs the split kernels, one chunk included (with a workspace).  Same argument contract
 // as fav4_bshd_forward_varlen (O and LSE rows, empty sequences, offset
 // clamping), plus:
 //  * splits: 0 = library choice (the chunk size the contiguous split-KV Auto
@@ -163,8 +168,9 @@ extern "C" int fav4_bshd_splitkv_varlen_select(const Fav4VarlenArgs* args, int c
 // packed sequences of 1-32 new queries (Q/O/LSE as in Fav4VarlenArgs), each
 // with its own number of cached keys, stored in fixed-size pages.  Key j of
 // sequence b is row block_table[b * max_pages_per_seq + j / page_size] *
-// page_size + j % page_size of the caches.  Dense only: causal must be 0 (a
-// top-left causal decode row would see only the first keys of its cache).
+// page_size + j % page_size of the caches.  causal is 0 (dense) or 2
+// (bottom-right, as for fav4_bshd_forward_splitkv_varlen); top-left (1) is
+// rejected, since a top-left decode row would see only its cache's first keys.
 // Runs the packed split-KV kernels (query heads of a K/V head share 32-row
 // tiles; chunks of a common number of key tiles, merged by log-sum-exp), so
 // per row the result is bitwise that of fav4_bshd_forward_splitkv_varlen on
@@ -184,7 +190,7 @@ struct Fav4PagedArgs {
     float scale;
 };
 // Checks (before any HIP call; hipErrorInvalidValue otherwise): the pointers,
-// sizes >= 1 (total_k >= 0), kv_heads dividing heads, causal = 0, a finite
+// sizes >= 1 (total_k >= 0), kv_heads dividing heads, causal 0 or 2, a finite
 // positive scale, max_seqlen_q <= 32, page_size a multiple of 32, max_seqlen_k
 // <= max_pages_per_seq * page_size and <= 2^19 (a chunk spans at most 64 key
 // tiles), page_size * kv_heads * 256 < 2^32, (heads / kv_heads) * max_seqlen_q

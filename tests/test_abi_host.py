@@ -441,9 +441,30 @@ def test_splitkv_varlen_rejects_bad_arguments(lib, name, change):
     assert lib.fav4_bshd_forward_splitkv_varlen(C.byref(a), 0, splits, 0x100000, 1 << 40, None) == \
         HIP_ERROR_INVALID_VALUE
     assert lib.fav4_bshd_forward_splitkv_varlen(None, 0, splits, 0x100000, 1 << 40, None) == HIP_ERROR_INVALID_VALUE
-    assert lib.fav4_bshd_forward_splitkv_varlen(C.byref(a), 2, 4, 0x100000, 1 << 40, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_forward_splitkv_varlen(C.byref(a), 3, 4, 0x100000, 1 << 40, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fav4_bshd_splitkv_varlen_select(None, 0) == -1
     assert lib.fav4_bshd_splitkv_varlen_workspace_size(None, 0, 0) == -1
+
+
+def test_splitkv_varlen_bottom_right(lib):
+    """causal = 2 (bottom-right) is planned like a dense call, always splits
+    (one chunk needs a workspace too) and is decode-only."""
+    f = _vgood()
+    f.update(q=None, k=None, v=None, o=None, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=4, max_seqlen_k=5000)
+    a = load_package().VarlenArgs(**f)
+    assert lib.fav4_bshd_splitkv_varlen_select(C.byref(a), 2) == lib.fav4_bshd_splitkv_varlen_select(C.byref(a), 0)
+    for splits in (0, 3):
+        dense = lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), 0, splits)
+        assert dense > 0 and lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), 2, splits) == dense
+    # one chunk: the dense call needs no workspace, bottom-right does
+    assert lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), 0, 1) == 0
+    assert lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), 2, 1) == 3 * 4 * 4 * 520
+    a.max_seqlen_q = 33
+    assert lib.fav4_bshd_splitkv_varlen_select(C.byref(a), 2) == -1
+    assert lib.fav4_bshd_splitkv_varlen_select(C.byref(a), 0) == 1
+    p = _pgood(q=None, k_cache=None, v_cache=None, o=None, cu_seqlens_q=None, seqlens_k=None, block_table=None)
+    assert lib.fav4_bshd_splitkv_paged_select(C.byref(p), 2) == lib.fav4_bshd_splitkv_paged_select(C.byref(p), 0) > 0
+    assert lib.fav4_bshd_splitkv_paged_select(C.byref(p), 1) == -1
 
 
 @pytest.mark.parametrize("ws,nbytes", [(None, 1 << 30), (0x100010, 1 << 30), (0x100000, 1000)],

@@ -211,3 +211,75 @@ def test_splitkv_paged_random(gpu_runner, case):
         got_lse = lse[:, a:b].cpu().numpy()[None] if with_lse else None
         e = orc.errors(to_host_bits(o[a:b])[None], got_lse, ref, ref_lse if with_lse else None)
         assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (i, sq, sk, e)
+
+
+def _bottom_right_ref(q, k, v, group):
+    """FP64 bottom-right causal (query i sees keys j <= sk - sq + i) from the
+    top-left oracle: queries padded in front to sk rows when sq <= sk, else
+    the rows that see keys are the last sk, top-left against all keys."""
+    sq, sk = len(q), len(k)
+    ke = np.repeat(k[None], group, axis=2)
+    ve = np.repeat(v[None], group, axis=2)
+    h = q.shape[1]
+    o = np.zeros((1, sq, h, 128))
+    lse = np.full((1, h, sq), -np.inf)
+    if sk == 0:
+        return o, lse
+    if sq <= sk:
+        qp = np.concatenate([np.zeros((sk - sq,) + q.shape[1:], dtype=q.dtype), q])[None]
+        ref, ref_lse = orc.attention_fp64(qp, ke, ve, orc.DEFAULT_SCALE, True)
+        return ref[:, sk - sq:], ref_lse[:, :, sk - sq:]
+    ref, ref_lse = orc.attention_fp64(q[sq - sk:][None], ke, ve, orc.DEFAULT_SCALE, True)
+    o[:, sq - sk:] = ref
+    lse[:, :, sq - sk:] = ref_lse
+    return o, lse
+
+
+@pytest.mark.parametrize("ps", [32, 128])
+def test_splitkv_bottom_right_causal(gpu_runner, ps):
+    """causal = 2 on the packed and the paged decode calls: the FP64 oracle
+    (bottom-right, including sequences with more queries than keys, whose
+    first rows see no key), and paged bitwise the packed call at the same
+    chunk count."""
+    import torch
+    h, kvh = 8, 2
+    lens = [(4, 3000), (1, 700), (32, 5000), (17, 17), (20, 9), (5, 0), (0, 40), (32, 65)]
+    q, k, v, kc, vc, cu_q, cu_k, seqlens_k, table = _build(h, kvh, ps, lens, seed=41)
+    dev = torch.device("cuda:0")
+    qd, kd, vd, kcd, vcd = (to_device(x, dev) for x in (q, k, v, kc, vc))
+    cq, ck, sk_d, tb = (torch.from_numpy(x).to(dev) for x in (cu_q, cu_k, seqlens_k, table))
+    max_q, max_k, tq, group = 32, 5000, len(q), h // kvh
+    for splits in (0, 1, 6):
+        print(f"  bottom-right causal page {ps} splits={splits}", flush=True)
+        ob, lb, o, lse = _out(torch, dev, tq, h, True)
+        gpu_runner.call_splitkv_varlen(qd, kd, vd, o, lse, cq, ck, max_q, max_k, 2, splits)
+        ob2, lb2, o2, lse2 = _out(torch, dev, tq, h, True)
+        gpu_runner.call_splitkv_paged(qd, kcd, vcd, o2, lse2, cq, sk_d, tb, max_q, max_k, splits, total_k=len(k),
+                                      causal=2)
+        torch.cuda.synchronize()
+        assert torch.isnan(ob[tq:]).all().item() and torch.isnan(lb[h * tq:]).all().item()
+        assert torch.isnan(ob2[tq:]).all().item() and torch.isnan(lb2[h * tq:]).all().item()
+        ws_v = gpu_runner.splitkv_varlen_workspace_size(len(lens), h, kvh, max_q, max_k, tq, len(k), 2, splits)
+        ws_p = gpu_runner.splitkv_paged_workspace_size(len(lens), h, kvh, max_q, max_k, tq, len(k), ps,
+                                                       table.shape[1], len(kc), splits)
+        if ws_v == ws_p:      # same plan (one explicit chunk over 157 key tiles: the paged cap makes 3)
+            assert torch.equal(o.view(torch.int16), o2.view(torch.int16)), splits
+            assert torch.equal(lse.view(torch.int32), lse2.view(torch.int32)), splits
+        for out_o, out_lse in ((o, lse), (o2, lse2)):
+            _check_bottom_right(out_o, out_lse, q, k, v, cu_q, cu_k, lens, group, splits)
+
+
+def _check_bottom_right(o, lse, q, k, v, cu_q, cu_k, lens, group, splits):
+    """Every sequence of a bottom-right causal output against the FP64 reference."""
+    for i, (sq, sk) in enumerate(lens):
+        a, b = cu_q[i], cu_q[i + 1]
+        c, d = cu_k[i], cu_k[i + 1]
+        if sq == 0:
+            continue
+        ref, ref_lse = _bottom_right_ref(q[a:b], k[c:d], v[c:d], group)
+        got, got_lse = to_host_bits(o[a:b])[None], lse[:, a:b].cpu().numpy()[None]
+        seen = np.isfinite(ref_lse[0, 0])                       # rows that see at least one key
+        assert (got_lse[:, :, ~seen] == -np.inf).all() and (orc.bf16_to_f32(got[:, ~seen]) == 0).all(), i
+        if seen.any():
+            e = orc.errors(got[:, seen], got_lse[:, :, seen], ref[:, seen], ref_lse[:, :, seen])
+            assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (splits, i, e)

@@ -286,3 +286,27 @@ def test_stress_pattern_counts():
     big_q = (np.abs(qf).max(axis=1) > 8).sum()
     big_k = (np.abs(kf).max(axis=1) > 30).sum()
     assert abs(big_q - 40) <= 2 and abs(big_k - 24) <= 1
+
+
+def test_bottom_right_reference_matches_direct_loop():
+    """The bottom-right causal reference of the decode tests (built from the
+    top-left oracle by padding) against a direct FP64 softmax per row: query i
+    sees keys j <= sk - sq + i, rows with no key give O = 0 and LSE = -inf."""
+    from tests.test_gpu_splitkv_paged import _bottom_right_ref
+    for sq, sk in [(4, 30), (20, 9), (17, 17), (1, 5), (3, 0)]:
+        q, _, _ = orc.make_inputs(1, 2, sq, max(sk, 1), "normal", seed=1)
+        _, k, v = orc.make_inputs(1, 2, sq, max(sk, 1), "normal", seed=2)
+        k, v = k[:, :sk], v[:, :sk]
+        o, lse = _bottom_right_ref(q[0], k[0], v[0], 1)
+        qf, kf, vf = (orc.bf16_to_f32(x).astype(np.float64) for x in (q[0], k[0], v[0]))
+        for i in range(sq):
+            lim = sk - sq + i
+            for hh in range(2):
+                if lim < 0:
+                    assert lse[0, hh, i] == -np.inf and (o[0, i, hh] == 0).all()
+                    continue
+                sc = kf[:lim + 1, hh] @ qf[i, hh] * orc.DEFAULT_SCALE
+                m = sc.max()
+                p = np.exp(sc - m)
+                assert np.allclose(o[0, i, hh], (p[:, None] * vf[:lim + 1, hh]).sum(0) / p.sum(), atol=1e-9)
+                assert abs(lse[0, hh, i] - (m + np.log(p.sum()))) < 1e-9
