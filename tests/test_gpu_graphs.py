@@ -118,3 +118,32 @@ def test_graph_varlen_and_strided(gpu_runner, causal):
     print(f"  graph strided causal={causal}", flush=True)
     _check_graph(torch, lambda: gpu_runner.call_strided(qb, kb, vb, ob.transpose(1, 2), None, causal, 0), [ob],
                  noise)
+
+
+
+def test_graph_paged_decode_bottom_right(gpu_runner):
+    """Split-KV decode over paged caches with the bottom-right mask: the page
+    lookup and both kernels replay to the eager result."""
+    import numpy as np
+    import torch
+    from tests.conftest import to_device
+    from tests.test_gpu_splitkv_paged import _build
+    h, kvh, ps = 16, 4, 64
+    lens = [(3, 2500), (1, 700), (8, 4100), (2, 0)]
+    q, k, _, kc, vc, cu_q, _, seqlens_k, table = _build(h, kvh, ps, lens, seed=51)
+    dev = torch.device("cuda:0")
+    qd, kcd, vcd = (to_device(x, dev) for x in (q, kc, vc))
+    cq, sk_d, tb = (torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in (cu_q, seqlens_k, table))
+    o = torch.empty_like(qd)
+    lse = torch.empty((h, len(q)), device="cuda", dtype=torch.float32)
+    on = torch.empty_like(qd)
+    need = max(gpu_runner.splitkv_paged_workspace_size(len(lens), h, kvh, 8, 4100, len(q), len(k), ps,
+                                                       table.shape[1], len(kc), s) for s in (7, 3))
+    ws = torch.empty(need, device="cuda", dtype=torch.uint8)
+
+    def call(out, out_lse, splits):
+        gpu_runner.call_splitkv_paged(qd, kcd, vcd, out, out_lse, cq, sk_d, tb, 8, 4100, splits, workspace=ws,
+                                      total_k=len(k), causal=2)
+
+    print("  graph paged decode bottom-right", flush=True)
+    _check_graph(torch, lambda: call(o, lse, 7), [o, lse], lambda: call(on, None, 3))
