@@ -239,7 +239,7 @@ int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, 
     const int64_t total = p.items * tiles * p.splits;
     const int64_t rows = int64_t(a.batch) * a.heads * a.sq;
     const bool decode = p.shape.bm == 32;
-    if (total > INT_MAX || rows > INT_MAX || (VARLEN && !decode) || (CAUSAL && !BR && decode))
+    if (total > INT_MAX || rows > INT_MAX || (VARLEN && !PAGED && !decode) || (CAUSAL && !BR && decode))
         return hipErrorInvalidValue;
     sp.o_part = static_cast<float*>(ws);
     sp.lse_part = sp.o_part + int64_t(p.splits) * rows * fav4::D;
@@ -251,8 +251,12 @@ int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, 
         hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, stream, a, sp, kv_heads, tiles, int(total));
     };
     if constexpr (VARLEN) {
-        if (a.lse) go(fav4::fwd_kernel_split<32, BR, 1, true, true, PAGED, BR>, 64);
-        else go(fav4::fwd_kernel_split<32, BR, 1, false, true, PAGED, BR>, 64);
+        if (decode && a.lse) go(fav4::fwd_kernel_split<32, BR, 1, true, true, PAGED, BR>, 64);
+        else if (decode) go(fav4::fwd_kernel_split<32, BR, 1, false, true, PAGED, BR>, 64);
+        if constexpr (PAGED) {      // prefill over paged caches: the 8-wave shape
+            if (!decode && a.lse) go(fav4::fwd_kernel_split<64, BR, 8, true, true, true, BR>, 512);
+            else if (!decode) go(fav4::fwd_kernel_split<64, BR, 8, false, true, true, BR>, 512);
+        }
     } else if constexpr (CAUSAL) {
         if (a.lse) go(fav4::fwd_kernel_split<64, true, 8, true>, 512);
         else go(fav4::fwd_kernel_split<64, true, 8, false>, 512);
@@ -383,10 +387,13 @@ int64_t varlen_workspace(const Fav4VarlenArgs& v, const SplitPlan& p, int causal
 constexpr int PAGED_MAX_TPS = 64;          // key tiles per chunk: one page number per lane
 constexpr int PAGED_MAX_KEYS = fav4::MAX_SPLITS * PAGED_MAX_TPS * 32;
 
+// Decode (max_seqlen_q <= 32) needs page_size % 32 == 0 (one 32-key tile per
+// page), prefill page_size % 64 == 0 (the 8-wave shape's 64-key tiles).
 int paged_shape_ok(const Fav4PagedArgs* a, int causal, int splits) {
     if (!a || a->batch <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads != 0 ||
-        a->max_seqlen_q <= 0 || a->max_seqlen_q > DECODE_SQ || a->max_seqlen_k <= 0 || a->total_q <= 0 ||
-        a->total_k < 0 || a->num_pages <= 0 || a->page_size <= 0 || a->page_size % 32 != 0 ||
+        a->max_seqlen_q <= 0 || a->max_seqlen_q > MAX_SPLIT_SQ || a->max_seqlen_k <= 0 || a->total_q <= 0 ||
+        a->total_k < 0 || a->num_pages <= 0 || a->page_size <= 0 ||
+        a->page_size % (a->max_seqlen_q > DECODE_SQ ? 64 : 32) != 0 ||
         a->max_pages_per_seq <= 0 || (causal != 0 && causal != BOTTOM_RIGHT) || !std::isfinite(a->scale) ||
         a->scale <= 0 || splits < 0 ||
         splits > fav4::MAX_SPLITS)
@@ -395,7 +402,8 @@ int paged_shape_ok(const Fav4PagedArgs* a, int causal, int splits) {
         int64_t(a->max_seqlen_k) > int64_t(a->max_pages_per_seq) * a->page_size ||
         int64_t(a->page_size) * a->kv_heads * 256 > int64_t(UINT32_MAX) ||
         int64_t(a->max_seqlen_q) * a->heads * 256 > int64_t(UINT32_MAX) ||
-        int64_t(a->heads / a->kv_heads) * a->max_seqlen_q * fav4::D * 4 > int64_t(UINT32_MAX) ||
+        (a->max_seqlen_q <= DECODE_SQ ? int64_t(a->heads / a->kv_heads) : 1) * a->max_seqlen_q * fav4::D * 4 >
+            int64_t(UINT32_MAX) ||
         int64_t(a->batch) * a->heads * a->max_seqlen_q > INT_MAX)
         return hipErrorInvalidValue;
     return hipSuccess;
@@ -424,9 +432,13 @@ Fav4Args paged_shape(const Fav4PagedArgs& v) {
 // The packed-batch plan, with chunks capped at 64 key tiles (a chunk's page
 // numbers fit the lanes of one wave); one chunk still runs the split kernels.
 SplitPlan paged_plan(const Fav4PagedArgs& v, int req) {
-    SplitPlan p = packed_split_plan(paged_shape(v), v.kv_heads, v.total_k, 0, req);
+    const Fav4Args a = paged_shape(v);
+    // Prefill: the contiguous prefill plan at the max lengths (bottom-right
+    // causal planned as dense: the last query sees every key).
+    SplitPlan p = a.sq > DECODE_SQ ? split_plan(a, v.kv_heads, 0, req)
+                                   : packed_split_plan(a, v.kv_heads, v.total_k, 0, req);
     if (p.tps > PAGED_MAX_TPS) {
-        const int ktiles = (v.max_seqlen_k + 31) / 32;
+        const int ktiles = (v.max_seqlen_k + p.shape.bn - 1) / p.shape.bn;
         p.tps = PAGED_MAX_TPS;
         p.splits = (ktiles + p.tps - 1) / p.tps;
     }

@@ -620,15 +620,15 @@ __device__ __forceinline__ SeqSpan seq_span(const SplitArgs& sp, int b, int max_
 // three workgroups share a CU and every resident wave computes.
 // LSE: keep the FP32 sums for the LSE output; without it the second log-sum
 // repeats the first (the merge reads it only when writing an LSE).
-// VARLEN: packed sequences (one wave only); a.sq / a.sk are the max lengths,
-// packed rows keep the a.sq stride, and rows past a sequence's own length are
-// computed on a valid query but never read by the merge.
+// VARLEN: packed sequences; a.sq / a.sk are the max lengths, rows keep the
+// a.sq stride, and rows past a sequence's own length are computed on a valid
+// query but never read by the merge (eight waves: q tiles past them exit).
 // PAGED (with VARLEN): K/V come from paged caches.  page_size is a multiple
 // of BN, so a key tile lies in one page; a chunk spans at most 64 pages, whose
 // (clamped) numbers one load puts in the wave's lanes at the chunk start.
-// BR (with CAUSAL, one wave): bottom-right causal, query i of a sequence with
-// sq queries and sk keys sees keys j <= sk - sq + i (the last query sees all
-// of them; with sq > sk the first sq - sk rows see none).
+// BR (with CAUSAL and VARLEN): bottom-right causal, query i of a sequence
+// with sq queries and sk keys sees keys j <= sk - sq + i (the last query sees
+// all of them; with sq > sk the first sq - sk rows see none).
 // The one-wave shape keeps the 8-wave shape's 256-register budget
 // (waves_per_eu 2); its occupancy is set by LDS (three workgroups per CU), so
 // the compiler's note that it cannot reach two waves per SIMD is expected.
@@ -637,9 +637,8 @@ __device__ __forceinline__ SeqSpan seq_span(const SplitArgs& sp, int b, int max_
 template <int BN, bool CAUSAL, int WAVES, bool LSE, bool VARLEN = false, bool PAGED = false, bool BR = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int total) {
-    static_assert(!VARLEN || WAVES == 1, "packed sequences use the one-wave shape");
     static_assert(!PAGED || VARLEN, "paged caches hold packed sequences");
-    static_assert(!BR || (CAUSAL && WAVES == 1), "bottom-right causal is a decode mask");
+    static_assert(!BR || (CAUSAL && VARLEN), "bottom-right causal needs per-sequence lengths");
     constexpr int BM = WAVES * 32, STAGES = 3;
     // One wave (decode): the q-tile rows are the group's query heads times
     // their sq queries, row r = (head - first head of the group) * sq + query,
@@ -708,7 +707,8 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
         SeqSpan span{a.sq, a.sk, int64_t(batch) * a.sq, int64_t(batch) * a.sk};
         if constexpr (VARLEN) {
             span = seq_span<PAGED>(sp, batch, a.sq, a.sk);
-            if (span.sq == 0) continue;                        // no query rows: nothing to merge
+            // No query rows (eight waves: none from this q tile on): nothing to merge.
+            if (span.sq == 0 || (!PACK && q0 >= span.sq)) continue;
         }
         const int sq = span.sq, sk = span.sk;
         // This lane's query position (causal limit) and Q byte offset inside
@@ -732,7 +732,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
         // every row below key sk - sq + 1 (query 0's first hidden key).
         const int kend = CAUSAL && !BR ? min(sk, PACK ? sq : q0 + BM) : sk;
         const int ntiles = (kend + BN - 1) / BN;
-        const int nfull = (BR ? max(0, sk - sq + 1) : CAUSAL ? (PACK ? 0 : min(sk, q0 + 1)) : sk) / BN;
+        const int nfull = (BR ? max(0, (PACK ? 0 : q0) + sk - sq + 1) : CAUSAL ? (PACK ? 0 : min(sk, q0 + 1)) : sk) / BN;
         const int climit = BR ? qi + sk - sq : qi;     // last visible key of this lane's row
         const int t0 = split * sp.tps, t1 = min(ntiles, t0 + sp.tps);
 
@@ -805,7 +805,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
             using Masked = std::integral_constant<bool, true>;
             int t = t0;
             const int tp = min(t1, nfull);
-            if (qw >= rows) {
+            if (qw >= (VARLEN && !PACK ? sq : rows)) {
                 // Rows all past sq (decode: 7 of 8 waves): only the DMA and
                 // barrier sequence of the loop below.
                 for (; t < t1; ++t) sync_and_prefetch(t);

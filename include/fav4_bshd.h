@@ -163,18 +163,22 @@ extern "C" int fav4_bshd_forward_splitkv_varlen(const Fav4VarlenArgs* args, int 
 extern "C" long long fav4_bshd_splitkv_varlen_workspace_size(const Fav4VarlenArgs* args, int causal, int splits);
 extern "C" int fav4_bshd_splitkv_varlen_select(const Fav4VarlenArgs* args, int causal);
 
-// ---- Paged K/V caches (decode) ------------------------------------------------
-// No counterpart in the reference.  The decode step over paged K/V caches:
-// packed sequences of 1-32 new queries (Q/O/LSE as in Fav4VarlenArgs), each
-// with its own number of cached keys, stored in fixed-size pages.  Key j of
+// ---- Paged K/V caches ---------------------------------------------------------
+// No counterpart in the reference.  Attention over paged K/V caches: packed
+// sequences of new queries (Q/O/LSE as in Fav4VarlenArgs; decode when
+// max_seqlen_q <= 32, else chunked prefill), each with its own number of
+// cached keys, stored in fixed-size pages.  Key j of
 // sequence b is row block_table[b * max_pages_per_seq + j / page_size] *
 // page_size + j % page_size of the caches.  causal is 0 (dense) or 2
 // (bottom-right, as for fav4_bshd_forward_splitkv_varlen); top-left (1) is
 // rejected, since a top-left decode row would see only its cache's first keys.
-// Runs the packed split-KV kernels (query heads of a K/V head share 32-row
-// tiles; chunks of a common number of key tiles, merged by log-sum-exp), so
-// per row the result is bitwise that of fav4_bshd_forward_splitkv_varlen on
-// the same keys stored contiguously, at the same chunk count.
+// Decode runs the packed split-KV kernels (query heads of a K/V head share
+// 32-row tiles; chunks of a common number of key tiles, merged by
+// log-sum-exp), so per row the result is bitwise that of
+// fav4_bshd_forward_splitkv_varlen on the same keys stored contiguously, at
+// the same chunk count.  Prefill runs the 8-wave split-KV kernels (256-row q
+// tiles, 64-key tiles) with the contiguous prefill plan at the max lengths,
+// bitwise fav4_bshd_forward_splitkv_gqa's on a batch of equal lengths.
 struct Fav4PagedArgs {
     const void *q;                     // BF16 [total_q, heads, 128], contiguous
     const void *k_cache, *v_cache;     // BF16 [num_pages, page_size, kv_heads, 128], contiguous
@@ -191,10 +195,12 @@ struct Fav4PagedArgs {
 };
 // Checks (before any HIP call; hipErrorInvalidValue otherwise): the pointers,
 // sizes >= 1 (total_k >= 0), kv_heads dividing heads, causal 0 or 2, a finite
-// positive scale, max_seqlen_q <= 32, page_size a multiple of 32, max_seqlen_k
-// <= max_pages_per_seq * page_size and <= 2^19 (a chunk spans at most 64 key
-// tiles), page_size * kv_heads * 256 < 2^32, (heads / kv_heads) * max_seqlen_q
-// < 2^23, 16-byte aligned Q/O/caches and 4-byte aligned int arrays and LSE.
+// positive scale, max_seqlen_q <= 2^22, page_size a multiple of 32 (decode)
+// or 64 (prefill), max_seqlen_k <= max_pages_per_seq * page_size and <= 2^19
+// (a chunk spans at most 64 key tiles), page_size * kv_heads * 256 < 2^32,
+// max_seqlen_q * heads * 256 < 2^32, for decode (heads / kv_heads) *
+// max_seqlen_q < 2^23, 16-byte aligned Q/O/caches and 4-byte aligned int
+// arrays and LSE.
 // Device-read values are clamped (query offsets to [0, total_q], key counts to
 // [0, max_seqlen_k], page numbers to [0, num_pages)), so malformed tables give
 // undefined results but no access outside the buffers.  A sequence with no

@@ -512,21 +512,30 @@ def _pgood(**kw):
 
 
 def _paged_plan(b, h, kvh, mq, mk, tk, splits):
-    """The packed-batch plan at these sizes with chunks capped at 64 key tiles."""
-    n, tps = _varlen_split_plan(b, h, kvh, mq, mk, tk, splits)
+    """Decode: the packed-batch plan at these sizes; prefill (mq > 32): the
+    contiguous dense plan at the max lengths; chunks capped at 64 key tiles
+    (32 keys decode, 64 prefill)."""
+    if mq > 32:
+        n, tps = _split_plan(b, h, mq, mk, splits, cus=256, kvh=kvh)
+        bn = 64
+    else:
+        n, tps = _varlen_split_plan(b, h, kvh, mq, mk, tk, splits)
+        bn = 32
     if tps > 64:
         tps = 64
-        n = -(-(-(-mk // 32)) // 64)
+        n = -(-(-(-mk // bn)) // 64)
     return n, tps
 
 
 @pytest.mark.parametrize("shape", [(8, 32, 8, 1, 32768, 8 * 4096), (1, 8, 8, 1, 65536, 65536), (3, 8, 2, 4, 5000, 9000),
                                    (16, 32, 4, 16, 2048, 16 * 1000), (1, 1, 1, 1, 524288, 524288),
-                                   (2, 4, 4, 32, 100, 3)])
+                                   (2, 4, 4, 32, 100, 3), (1, 8, 2, 1000, 32768, 32768), (3, 4, 4, 300, 5000, 9000),
+                                   (1, 1, 1, 4096, 524288, 524288)])
 def test_splitkv_paged_plan(lib, shape):
     b, h, kvh, mq, mk, tk = shape
+    ps = 32 if mq <= 32 else 64
     a = _pgood(batch=b, heads=h, kv_heads=kvh, max_seqlen_q=mq, max_seqlen_k=mk, total_k=tk, total_q=b * mq,
-               page_size=32, max_pages_per_seq=-(-mk // 32), q=None, k_cache=None, v_cache=None, o=None,
+               page_size=ps, max_pages_per_seq=-(-mk // ps), q=None, k_cache=None, v_cache=None, o=None,
                cu_seqlens_q=None, seqlens_k=None, block_table=None)
     n, tps = _paged_plan(b, h, kvh, mq, mk, tk, 0)
     assert tps <= 64
@@ -541,7 +550,8 @@ def test_splitkv_paged_plan(lib, shape):
 PBAD = [("q_null", dict(q=None)), ("k_null", dict(k_cache=None)), ("v_null", dict(v_cache=None)),
         ("o_null", dict(o=None)), ("cuq_null", dict(cu_seqlens_q=None)), ("seqk_null", dict(seqlens_k=None)),
         ("table_null", dict(block_table=None)), ("batch0", dict(batch=0)), ("heads0", dict(heads=0)),
-        ("kv3", dict(kv_heads=3)), ("maxq0", dict(max_seqlen_q=0)), ("maxq33", dict(max_seqlen_q=33)),
+        ("kv3", dict(kv_heads=3)), ("maxq0", dict(max_seqlen_q=0)), ("prefill_page32", dict(max_seqlen_q=33, page_size=32)),
+        ("maxq_2p22", dict(max_seqlen_q=(1 << 22) + 1, heads=2, kv_heads=2, total_q=1 << 23)),
         ("maxk0", dict(max_seqlen_k=0)), ("totq0", dict(total_q=0)), ("totk_neg", dict(total_k=-1)),
         ("pages0", dict(num_pages=0)), ("page16", dict(page_size=16)), ("page48", dict(page_size=48)),
         ("maxpages0", dict(max_pages_per_seq=0)), ("table_short", dict(max_pages_per_seq=78)),

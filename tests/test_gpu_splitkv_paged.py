@@ -283,3 +283,55 @@ def _check_bottom_right(o, lse, q, k, v, cu_q, cu_k, lens, group, splits):
         if seen.any():
             e = orc.errors(got[:, seen], got_lse[:, :, seen], ref[:, seen], ref_lse[:, :, seen])
             assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (splits, i, e)
+
+
+@pytest.mark.parametrize("ps", [64, 256])
+def test_splitkv_paged_prefill(gpu_runner, ps):
+    """Queries longer than 32 over paged caches (the 8-wave shape): dense and
+    bottom-right causal against the FP64 oracle on ragged batches (several q
+    tiles, q tiles past short sequences, sq > sk), and a uniform batch bitwise
+    the contiguous split-KV at the same chunk count."""
+    import torch
+    h, kvh = 8, 2
+    group = h // kvh
+    dev = torch.device("cuda:0")
+    lens = [(600, 3000), (33, 700), (300, 300), (64, 20), (0, 100), (1, 4100)]
+    q, k, v, kc, vc, cu_q, cu_k, seqlens_k, table = _build(h, kvh, ps, lens, seed=61)
+    qd, kcd, vcd = (to_device(x, dev) for x in (q, kc, vc))
+    cq, sk_d, tb = (torch.from_numpy(x).to(dev) for x in (cu_q, seqlens_k, table))
+    max_q, max_k, tq = 600, 4100, len(q)
+    for causal, splits in ((0, 0), (0, 5), (2, 0), (2, 3)):
+        print(f"  paged prefill page {ps} causal={causal} splits={splits}", flush=True)
+        ob, lb, o, lse = _out(torch, dev, tq, h, True)
+        gpu_runner.call_splitkv_paged(qd, kcd, vcd, o, lse, cq, sk_d, tb, max_q, max_k, splits, total_k=len(k),
+                                      causal=causal)
+        torch.cuda.synchronize()
+        assert torch.isnan(ob[tq:]).all().item() and torch.isnan(lb[h * tq:]).all().item()
+        if causal == 2:
+            _check_bottom_right(o, lse, q, k, v, cu_q, cu_k, lens, group, splits)
+            continue
+        for i, (sq, sk) in enumerate(lens):
+            a, b = cu_q[i], cu_q[i + 1]
+            c, d = cu_k[i], cu_k[i + 1]
+            if sq == 0:
+                continue
+            ke = np.repeat(k[c:d][None], group, axis=2)
+            ve = np.repeat(v[c:d][None], group, axis=2)
+            ref, ref_lse = orc.attention_fp64(q[a:b][None], ke, ve, orc.DEFAULT_SCALE, False)
+            e = orc.errors(to_host_bits(o[a:b])[None], lse[:, a:b].cpu().numpy()[None], ref, ref_lse)
+            assert orc.check_acceptance_tolerance(e) and orc.check_reference_tolerance(e), (splits, i, e)
+
+    # uniform batch: bitwise the contiguous (BSHD) split-KV at the same chunk count
+    b, sq, sk, splits = 3, 300, 2500, 4
+    q, k, v, kc, vc, cu_q, cu_k, seqlens_k, table = _build(h, kvh, ps, [(sq, sk)] * b, seed=62)
+    qd, kd, vd, kcd, vcd = (to_device(x, dev) for x in (q, k, v, kc, vc))
+    cq, sk_d, tb = (torch.from_numpy(x).to(dev) for x in (cu_q, seqlens_k, table))
+    _, _, o, lse = _out(torch, dev, b * sq, h, True)
+    gpu_runner.call_splitkv_paged(qd, kcd, vcd, o, lse, cq, sk_d, tb, sq, sk, splits, total_k=b * sk)
+    oc = torch.full((b, sq, h, 128), float("nan"), device=dev, dtype=torch.bfloat16)
+    lc = torch.full((b, h, sq), float("nan"), device=dev, dtype=torch.float32)
+    gpu_runner.call_splitkv(qd.view(b, sq, h, 128), kd.view(b, sk, kvh, 128), vd.view(b, sk, kvh, 128), oc, lc,
+                            False, splits)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), oc.view(-1, h, 128).view(torch.int16))
+    assert torch.equal(lse.view(torch.int32), lc.permute(1, 0, 2).reshape(h, b * sq).view(torch.int32))
