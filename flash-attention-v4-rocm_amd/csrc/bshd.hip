@@ -239,7 +239,7 @@ int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, 
     const int64_t total = p.items * tiles * p.splits;
     const int64_t rows = int64_t(a.batch) * a.heads * a.sq;
     const bool decode = p.shape.bm == 32;
-    if (total > INT_MAX || rows > INT_MAX || (VARLEN && !PAGED && !decode) || (CAUSAL && !BR && decode))
+    if (total > INT_MAX || rows > INT_MAX || (VARLEN && !PAGED && !BR && !decode) || (CAUSAL && !BR && decode))
         return hipErrorInvalidValue;
     sp.o_part = static_cast<float*>(ws);
     sp.lse_part = sp.o_part + int64_t(p.splits) * rows * fav4::D;
@@ -253,9 +253,9 @@ int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, 
     if constexpr (VARLEN) {
         if (decode && a.lse) go(fav4::fwd_kernel_split<32, BR, 1, true, true, PAGED, BR>, 64);
         else if (decode) go(fav4::fwd_kernel_split<32, BR, 1, false, true, PAGED, BR>, 64);
-        if constexpr (PAGED) {      // prefill over paged caches: the 8-wave shape
-            if (!decode && a.lse) go(fav4::fwd_kernel_split<64, BR, 8, true, true, true, BR>, 512);
-            else if (!decode) go(fav4::fwd_kernel_split<64, BR, 8, false, true, true, BR>, 512);
+        if constexpr (PAGED || BR) {  // prefill over paged caches or with the bottom-right mask: 8 waves
+            if (!decode && a.lse) go(fav4::fwd_kernel_split<64, BR, 8, true, true, PAGED, BR>, 512);
+            else if (!decode) go(fav4::fwd_kernel_split<64, BR, 8, false, true, PAGED, BR>, 512);
         }
     } else if constexpr (CAUSAL) {
         if (a.lse) go(fav4::fwd_kernel_split<64, true, 8, true>, 512);
@@ -364,7 +364,10 @@ SplitPlan packed_split_plan(const Fav4Args& a, int kv_heads, int64_t total_k, in
 constexpr int BOTTOM_RIGHT = 2;
 
 SplitPlan varlen_split_plan(const Fav4VarlenArgs& v, int causal, int req) {
-    return packed_split_plan(varlen_shape(v), v.kv_heads, v.total_k, causal == BOTTOM_RIGHT ? 0 : causal, req);
+    const Fav4Args a = varlen_shape(v);
+    // Bottom-right prefill: the contiguous prefill plan at the max lengths.
+    if (causal == BOTTOM_RIGHT && a.sq > DECODE_SQ) return split_plan(a, v.kv_heads, 0, req);
+    return packed_split_plan(a, v.kv_heads, v.total_k, causal == BOTTOM_RIGHT ? 0 : causal, req);
 }
 
 int varlen_split_ok(const Fav4VarlenArgs* v, int causal, int splits, bool buffers) {
@@ -372,7 +375,7 @@ int varlen_split_ok(const Fav4VarlenArgs* v, int causal, int splits, bool buffer
     const int st = buffers ? varlen_ok(v, br ? 0 : causal) : varlen_shape_ok(v, br ? 0 : causal);
     if (st != hipSuccess) return st;
     if (splits < 0 || splits > fav4::MAX_SPLITS) return hipErrorInvalidValue;
-    if (v->max_seqlen_q > DECODE_SQ) return br ? hipErrorInvalidValue : hipSuccess;
+    if (v->max_seqlen_q > DECODE_SQ && !br) return hipSuccess;
     const Fav4Args a = varlen_shape(*v);
     return split_shape_ok(&a, v->kv_heads, br ? 0 : causal, splits);
 }

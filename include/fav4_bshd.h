@@ -141,11 +141,12 @@ extern "C" int fav4_bshd_forward_varlen(const Fav4VarlenArgs* args, int causal, 
 // the same chunk count.  Anything else (max_seqlen_q > 32, or causal = 1:
 // top-left causal decode sees at most 32 keys) takes one chunk, i.e. runs
 // fav4_bshd_forward_varlen, and needs no workspace.
-// causal = 2 (these calls and the paged ones only; max_seqlen_q <= 32):
-// bottom-right causal, query i of a sequence with sq queries and sk keys sees
-// keys j <= sk - sq + i (the last query sees them all; with sq > sk the first
-// sq - sk rows see none: O = 0, LSE = -inf).  It is planned like a dense call
-// and always runs the split kernels, one chunk included (with a workspace).  Same argument contract
+// causal = 2 (these calls and the paged ones only): bottom-right causal,
+// query i of a sequence with sq queries and sk keys sees keys j <= sk - sq + i
+// (the last query sees them all; with sq > sk the first sq - sk rows see
+// none: O = 0, LSE = -inf).  It is planned like a dense call (max_seqlen_q >
+// 32: the contiguous prefill plan at the max lengths, 8-wave kernels) and
+// always runs the split kernels, one chunk included (with a workspace).  Same argument contract
 // as fav4_bshd_forward_varlen (O and LSE rows, empty sequences, offset
 // clamping), plus:
 //  * splits: 0 = library choice (the chunk size the contiguous split-KV Auto

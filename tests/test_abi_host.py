@@ -447,8 +447,9 @@ def test_splitkv_varlen_rejects_bad_arguments(lib, name, change):
 
 
 def test_splitkv_varlen_bottom_right(lib):
-    """causal = 2 (bottom-right) is planned like a dense call, always splits
-    (one chunk needs a workspace too) and is decode-only."""
+    """causal = 2 (bottom-right) is planned like a dense call and always
+    splits (one chunk needs a workspace too); longer queries take the dense
+    prefill plan."""
     f = _vgood()
     f.update(q=None, k=None, v=None, o=None, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=4, max_seqlen_k=5000)
     a = load_package().VarlenArgs(**f)
@@ -459,8 +460,11 @@ def test_splitkv_varlen_bottom_right(lib):
     # one chunk: the dense call needs no workspace, bottom-right does
     assert lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), 0, 1) == 0
     assert lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), 2, 1) == 3 * 4 * 4 * 520
-    a.max_seqlen_q = 33
-    assert lib.fav4_bshd_splitkv_varlen_select(C.byref(a), 2) == -1
+    # prefill: the contiguous dense prefill plan at the max lengths, with a workspace
+    a.max_seqlen_q = 600
+    n, _ = _split_plan(3, 4, 600, 5000, 0, cus=256, kvh=2)
+    assert lib.fav4_bshd_splitkv_varlen_select(C.byref(a), 2) == n
+    assert lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), 2, 0) == n * 3 * 4 * 600 * 520
     assert lib.fav4_bshd_splitkv_varlen_select(C.byref(a), 0) == 1
     p = _pgood(q=None, k_cache=None, v_cache=None, o=None, cu_seqlens_q=None, seqlens_k=None, block_table=None)
     assert lib.fav4_bshd_splitkv_paged_select(C.byref(p), 2) == lib.fav4_bshd_splitkv_paged_select(C.byref(p), 0) > 0

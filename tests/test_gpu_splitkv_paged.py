@@ -309,6 +309,19 @@ def test_splitkv_paged_prefill(gpu_runner, ps):
         assert torch.isnan(ob[tq:]).all().item() and torch.isnan(lb[h * tq:]).all().item()
         if causal == 2:
             _check_bottom_right(o, lse, q, k, v, cu_q, cu_k, lens, group, splits)
+            # the contiguous packed call: the same rows, bitwise when the plans agree
+            kd, vd = to_device(k, dev), to_device(v, dev)
+            _, _, o2, lse2 = _out(torch, dev, tq, h, True)
+            gpu_runner.call_splitkv_varlen(qd, kd, vd, o2, lse2, cq, torch.from_numpy(cu_k).to(dev), max_q, max_k,
+                                           2, splits)
+            torch.cuda.synchronize()
+            _check_bottom_right(o2, lse2, q, k, v, cu_q, cu_k, lens, group, splits)
+            ws_v = gpu_runner.splitkv_varlen_workspace_size(len(lens), h, kvh, max_q, max_k, tq, len(k), 2, splits)
+            ws_p = gpu_runner.splitkv_paged_workspace_size(len(lens), h, kvh, max_q, max_k, tq, len(k), ps,
+                                                           table.shape[1], len(kc), splits)
+            if ws_v == ws_p:
+                assert torch.equal(o.view(torch.int16), o2.view(torch.int16)), splits
+                assert torch.equal(lse.view(torch.int32), lse2.view(torch.int32)), splits
             continue
         for i, (sq, sk) in enumerate(lens):
             a, b = cu_q[i], cu_q[i + 1]
