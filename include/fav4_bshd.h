@@ -138,9 +138,9 @@ extern "C" int fav4_bshd_forward_varlen(const Fav4VarlenArgs* args, int causal, 
 // common number of key tiles (a sequence gets as many chunks as its keys
 // need), merged by their log-sum-exp as in fav4_bshd_forward_splitkv_gqa;
 // with equal lengths the result is bitwise that call's on the same data at
-// the same chunk count.  Anything else (max_seqlen_q > 32, or causal = 1:
-// top-left causal decode sees at most 32 keys) takes one chunk, i.e. runs
-// fav4_bshd_forward_varlen, and needs no workspace.
+// the same chunk count.  Otherwise, for causal 0 or 1 (max_seqlen_q > 32,
+// or causal = 1: top-left causal decode sees at most 32 keys), the call takes
+// one chunk, i.e. runs fav4_bshd_forward_varlen, and needs no workspace.
 // causal = 2 (these calls and the paged ones only): bottom-right causal,
 // query i of a sequence with sq queries and sk keys sees keys j <= sk - sq + i
 // (the last query sees them all; with sq > sk the first sq - sk rows see
