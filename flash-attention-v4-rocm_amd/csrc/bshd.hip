@@ -44,13 +44,17 @@ int dispatch(const Fav4Args& a, const fav4::Layout& L, int config, hipStream_t s
 }
 
 // Argument checks of src/bshd.hip:27-34, in the same order, before any HIP call.
-int validate(const Fav4Args* a, int causal, int config) {
+// kv_heads: heads of K/V (0 = heads, the reference's case); the key-side
+// overflow limit counts those, as K/V rows are kv_heads * 256 bytes apart.
+int validate(const Fav4Args* a, int causal, int config, int kv_heads = 0) {
     if (!a || !a->q || !a->k || !a->v || !a->o || a->batch <= 0 || a->heads <= 0 || a->sq <= 0 ||
         a->sk <= 0 || (causal != 0 && causal != 1) || config < 0 || config > 3 ||
         !std::isfinite(a->scale) || a->scale <= 0)
         return hipErrorInvalidValue;
+    if (kv_heads == 0) kv_heads = a->heads;
+    if (kv_heads < 0 || kv_heads > a->heads || a->heads % kv_heads != 0) return hipErrorInvalidValue;
     if (a->batch > INT_MAX / a->heads || a->heads > INT_MAX / 128 ||
-        a->sq > INT_MAX / (a->heads * 128) || a->sk > INT_MAX / (a->heads * 128) ||
+        a->sq > INT_MAX / (a->heads * 128) || a->sk > INT_MAX / (kv_heads * 128) ||
         ((reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->k) |
           reinterpret_cast<uintptr_t>(a->v) | reinterpret_cast<uintptr_t>(a->o)) & 15))
         return hipErrorInvalidValue;
@@ -133,12 +137,16 @@ int device_cus() {
 //  * split: rounds * (F + c per 64-key tile of a chunk) + 5 for the merge,
 //    F = 19 and c = 1.8 dense, F = 18 and c = 1.5 causal;
 // where rounds = work items / resident workgroups, rounded up.
-int prefill_auto_splits(const Fav4Args& a, int causal, int max_splits, int ktiles) {
+int prefill_auto_splits(const Fav4Args& a, int causal, int max_splits, int ktiles, bool br) {
     const int64_t cus = device_cus();
     const int64_t bh = int64_t(a.batch) * a.heads;
     const int keys = causal ? std::min(a.sk, a.sq) : a.sk;
+    // Key tiles visible to a q tile whose rows end at rows_end (bottom-right:
+    // the last row sees keys up to rows_end - 1 + sk - sq).
     auto vis_tiles = [&](int64_t rows_end) {
-        return int((std::min<int64_t>(keys, causal ? rows_end : keys) + 63) / 64);
+        int64_t vis = causal ? std::min<int64_t>(keys, rows_end) : keys;
+        if (br) vis = std::min<int64_t>(keys, std::max<int64_t>(0, std::min<int64_t>(rows_end, a.sq) + a.sk - a.sq));
+        return int((vis + 63) / 64);
     };
     const int nt128 = (a.sq + 127) / 128;
     double best;
@@ -154,14 +162,20 @@ int prefill_auto_splits(const Fav4Args& a, int causal, int max_splits, int ktile
         const int64_t items = bh * nt128;
         best = double((items + 2 * cus - 1) / (2 * cus)) * (9.0 + (items <= cus ? 0.9 : 1.0) * ktiles);
     }
-    const double fixed = causal ? 18.0 : 19.0, per_tile = causal ? 1.5 : 1.8;
-    int pick = 1;
+    const double fixed = causal || br ? 18.0 : 19.0, per_tile = causal || br ? 1.5 : 1.8;
     const int nt256 = (a.sq + 255) / 256;
-    for (int s = 2; s <= max_splits; ++s) {
+    auto split_time = [&](int s) {
         const int tps = (ktiles + s - 1) / s;
         int64_t items = 0;
         for (int i = 0; i < nt256; ++i) items += (vis_tiles(256LL * (i + 1)) + tps - 1) / tps;
-        const double t = double((bh * items + cus - 1) / cus) * (fixed + per_tile * tps) + 5.0;
+        return double((bh * items + cus - 1) / cus) * (fixed + per_tile * tps) + 5.0;
+    };
+    // Bottom-right causal has no unsplit kernel: one chunk runs the split
+    // kernels too, so it competes under the split model.
+    if (br) best = split_time(1);
+    int pick = 1;
+    for (int s = 2; s <= max_splits; ++s) {
+        const double t = split_time(s);
         if (t < best) best = t, pick = s;
     }
     return pick;
@@ -174,7 +188,7 @@ int prefill_auto_splits(const Fav4Args& a, int causal, int max_splits, int ktile
 // count is then rounded so that no chunk starts past that range.
 // The decode shape packs the query heads that share a K/V head into one row
 // space of (heads / kv_heads) * sq rows per (batch, K/V head).
-SplitPlan split_plan(const Fav4Args& a, int kv_heads, int causal, int req) {
+SplitPlan split_plan(const Fav4Args& a, int kv_heads, int causal, int req, bool br = false) {
     const SplitShape sh = split_shape(a);
     const bool pack = sh.bm == 32;
     const int rows = pack ? (a.heads / kv_heads) * a.sq : a.sq;
@@ -192,7 +206,7 @@ SplitPlan split_plan(const Fav4Args& a, int kv_heads, int causal, int req) {
         const int auto_max = pack && units <= 2 ? fav4::MAX_SPLITS : sh.auto_max;
         splits = (int64_t(device_cus()) * sh.wgs_per_cu + units - 1) / units;
         splits = std::min<int64_t>(splits, std::min(auto_max, std::max(1, ktiles / MIN_TILES_PER_SPLIT)));
-        if (!pack && splits > 1) splits = prefill_auto_splits(a, causal, int(splits), ktiles);
+        if (!pack && splits > 1) splits = prefill_auto_splits(a, causal, int(splits), ktiles, br);
     }
     splits = std::max<int64_t>(1, std::min<int64_t>(splits, ktiles));
     const int tps = int((ktiles + splits - 1) / splits);
@@ -207,9 +221,9 @@ int64_t split_workspace(const Fav4Args& a, const SplitPlan& p) {
 // Shape-only checks for the split-KV queries (no buffers needed yet).
 int split_shape_ok(const Fav4Args* a, int kv_heads, int causal, int splits) {
     if (!a || a->batch <= 0 || a->heads <= 0 || a->sq <= 0 || a->sk <= 0 || (causal != 0 && causal != 1) ||
+        kv_heads <= 0 || kv_heads > a->heads || a->heads % kv_heads != 0 ||
         a->batch > INT_MAX / a->heads || a->heads > INT_MAX / 128 || a->sq > INT_MAX / (a->heads * 128) ||
-        a->sk > INT_MAX / (a->heads * 128) || splits < 0 || splits > fav4::MAX_SPLITS || a->sq > MAX_SPLIT_SQ ||
-        kv_heads <= 0 || kv_heads > a->heads || a->heads % kv_heads != 0)
+        a->sk > INT_MAX / (kv_heads * 128) || splits < 0 || splits > fav4::MAX_SPLITS || a->sq > MAX_SPLIT_SQ)
         return hipErrorInvalidValue;
     // Decode packs a group's (heads / kv_heads) * sq rows into one row space,
     // whose FP32 partial rows must fit a 4 GiB buffer bound.
@@ -219,7 +233,8 @@ int split_shape_ok(const Fav4Args* a, int kv_heads, int causal, int splits) {
 }
 
 int split_args_ok(const Fav4Args* a, int kv_heads, int causal, int splits) {
-    const int st = validate(a, causal, 0);
+    if (kv_heads <= 0) return hipErrorInvalidValue;
+    const int st = validate(a, causal, 0, kv_heads);
     return st != hipSuccess ? st : split_shape_ok(a, kv_heads, causal, splits);
 }
 
@@ -366,7 +381,7 @@ constexpr int BOTTOM_RIGHT = 2;
 SplitPlan varlen_split_plan(const Fav4VarlenArgs& v, int causal, int req) {
     const Fav4Args a = varlen_shape(v);
     // Bottom-right prefill: the contiguous prefill plan at the max lengths.
-    if (causal == BOTTOM_RIGHT && a.sq > DECODE_SQ) return split_plan(a, v.kv_heads, 0, req);
+    if (causal == BOTTOM_RIGHT && a.sq > DECODE_SQ) return split_plan(a, v.kv_heads, 0, req, true);
     return packed_split_plan(a, v.kv_heads, v.total_k, causal == BOTTOM_RIGHT ? 0 : causal, req);
 }
 
@@ -434,11 +449,11 @@ Fav4Args paged_shape(const Fav4PagedArgs& v) {
 
 // The packed-batch plan, with chunks capped at 64 key tiles (a chunk's page
 // numbers fit the lanes of one wave); one chunk still runs the split kernels.
-SplitPlan paged_plan(const Fav4PagedArgs& v, int req) {
+SplitPlan paged_plan(const Fav4PagedArgs& v, int causal, int req) {
     const Fav4Args a = paged_shape(v);
     // Prefill: the contiguous prefill plan at the max lengths (bottom-right
-    // causal planned as dense: the last query sees every key).
-    SplitPlan p = a.sq > DECODE_SQ ? split_plan(a, v.kv_heads, 0, req)
+    // causal with the key count its q tiles see).
+    SplitPlan p = a.sq > DECODE_SQ ? split_plan(a, v.kv_heads, 0, req, causal == BOTTOM_RIGHT)
                                    : packed_split_plan(a, v.kv_heads, v.total_k, 0, req);
     if (p.tps > PAGED_MAX_TPS) {
         const int ktiles = (v.max_seqlen_k + p.shape.bn - 1) / p.shape.bn;
@@ -535,9 +550,9 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_varlen(c
 // Grouped-query / multi-query attention (no counterpart in the reference).
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_gqa(const Fav4Args* a, int kv_heads,
                                                                     int causal, int config, hipStream_t stream) {
-    const int st = validate(a, causal, config);
+    if (kv_heads <= 0) return hipErrorInvalidValue;
+    const int st = validate(a, causal, config, kv_heads);
     if (st != hipSuccess) return st;
-    if (kv_heads <= 0 || kv_heads > a->heads || a->heads % kv_heads != 0) return hipErrorInvalidValue;
     if (config == 0) config = auto_config(*a, causal);
     const fav4::Layout L = bshd_layout(*a, kv_heads);
     return causal ? dispatch<true>(*a, L, config, stream) : dispatch<false>(*a, L, config, stream);
@@ -635,13 +650,13 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_splitkv_paged_select(const Fav4PagedArgs* a,
                                                                              int causal) {
     if (paged_shape_ok(a, causal, 0) != hipSuccess) return -1;
-    return paged_plan(*a, 0).splits;
+    return paged_plan(*a, causal, 0).splits;
 }
 
 extern "C" __attribute__((visibility("default"))) long long fav4_bshd_splitkv_paged_workspace_size(
     const Fav4PagedArgs* a, int causal, int splits) {
     if (paged_shape_ok(a, causal, splits) != hipSuccess) return -1;
-    return paged_workspace(*a, paged_plan(*a, splits));
+    return paged_workspace(*a, paged_plan(*a, causal, splits));
 }
 
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_paged(const Fav4PagedArgs* a,
@@ -651,7 +666,7 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_
                                                                               hipStream_t stream) {
     const int st = paged_ok(a, causal, splits);
     if (st != hipSuccess) return st;
-    const SplitPlan p = paged_plan(*a, splits);
+    const SplitPlan p = paged_plan(*a, causal, splits);
     const int64_t need = paged_workspace(*a, p);
     if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || uint64_t(need) > workspace_bytes)
         return hipErrorInvalidValue;

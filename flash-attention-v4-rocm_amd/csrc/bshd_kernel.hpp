@@ -529,21 +529,27 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
             }
         }
 
-        // Epilogue: O = acc / lb in BF16; rows >= sq fall outside the store bound.
+        // Epilogue: O = acc / lb in BF16.
         // Dividing by the sum of the rounded weights keeps them normalised, so
         // the BF16 rounding of P perturbs O by sum_j w_j e_j (V_j - O) instead
         // of sum_j w_j e_j V_j (exact when one key dominates).
+        // Rows >= sq store nothing.  The store bound alone does not stop them:
+        // their 32-bit offsets (row - q0) * row stride can wrap past 2^32 into
+        // a valid row when the row stride is large (huge head counts, strided
+        // views), and they carry another row's result.
         const float inv = 1.f / st.lb;
         const uint32_t obase = uint32_t(wave * 32 + col) * L.orow + half * 8;
+        if (row < a.sq) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+            for (int db = 0; db < 4; ++db) {
 #pragma unroll
-            for (int vg = 0; vg < 4; ++vg) {
-                const f32x2 x0 = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv};
-                const f32x2 x1 = {st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
-                const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
-                const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
-                store8(ro, obase + (db * 32 + vg * 8) * 2, bf16x4{y0[0], y0[1], y1[0], y1[1]});
+                for (int vg = 0; vg < 4; ++vg) {
+                    const f32x2 x0 = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv};
+                    const f32x2 x1 = {st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
+                    const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
+                    const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
+                    store8(ro, obase + (db * 32 + vg * 8) * 2, bf16x4{y0[0], y0[1], y1[0], y1[1]});
+                }
             }
         }
         // An explicit FMA: every kernel rounds the LSE the same way, whatever
@@ -728,9 +734,13 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
         const rsrc_t rp = make_rsrc(sp.o_part + prow0 * D, uint32_t(rows - q0) * D * 4);
         // PACK: every q tile holds rows of query 0 and of the last query, so
         // the causal range is the whole [0, min(sk, sq)) and no tile is
-        // unmasked for every row.  BR: the range is [0, sk), unmasked for
-        // every row below key sk - sq + 1 (query 0's first hidden key).
-        const int kend = CAUSAL && !BR ? min(sk, PACK ? sq : q0 + BM) : sk;
+        // unmasked for every row.  BR: unmasked for every row below key
+        // sk - sq + 1 (query 0's first hidden key); PACK sees [0, sk) (its
+        // tile holds the last query), a q tile of rows [q0, q0 + BM) only up
+        // to its last row's diagonal, so chunks past it are empty.
+        const int kend = !CAUSAL ? sk
+                         : BR    ? (PACK ? sk : min(sk, max(0, min(sq, q0 + BM) + sk - sq)))
+                                 : min(sk, PACK ? sq : q0 + BM);
         const int ntiles = (kend + BN - 1) / BN;
         const int nfull = (BR ? max(0, (PACK ? 0 : q0) + sk - sq + 1) : CAUSAL ? (PACK ? 0 : min(sk, q0 + 1)) : sk) / BN;
         const int climit = BR ? qi + sk - sq : qi;     // last visible key of this lane's row
@@ -1010,18 +1020,22 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
             }
         }
 
-        // O = acc / lb (0 for a sequence without keys), BF16.
+        // O = acc / lb (0 for a sequence without keys), BF16.  Rows past the
+        // sequence store nothing (their 32-bit offsets can wrap into a valid
+        // row when heads * 256 bytes is large).
         const float inv = st.lb > 0.f ? 1.f / st.lb : 0.f;
         const uint32_t obase = uint32_t(wave * 32 + col) * row_bytes + half * 8;
+        if (row < sq) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+            for (int db = 0; db < 4; ++db) {
 #pragma unroll
-            for (int vg = 0; vg < 4; ++vg) {
-                const f32x2 x0 = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv};
-                const f32x2 x1 = {st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
-                const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
-                const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
-                store8(ro, obase + (db * 32 + vg * 8) * 2, bf16x4{y0[0], y0[1], y1[0], y1[1]});
+                for (int vg = 0; vg < 4; ++vg) {
+                    const f32x2 x0 = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv};
+                    const f32x2 x1 = {st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
+                    const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
+                    const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
+                    store8(ro, obase + (db * 32 + vg * 8) * 2, bf16x4{y0[0], y0[1], y1[0], y1[1]});
+                }
             }
         }
         if constexpr (LSE) {

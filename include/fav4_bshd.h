@@ -98,7 +98,9 @@ extern "C" int fav4_bshd_splitkv_gqa_select(const Fav4Args* args, int kv_heads, 
 // [batch, sk, kv_heads, 128] with kv_heads dividing heads: query head h reads
 // K/V head h / (heads / kv_heads).  kv_heads == heads is exactly
 // fav4_bshd_forward.  Returns hipErrorInvalidValue also for kv_heads <= 0,
-// kv_heads > heads or heads % kv_heads != 0.
+// kv_heads > heads or heads % kv_heads != 0.  The key-side overflow limit
+// counts the K/V heads: sk * kv_heads * 128 must stay below 2^31 (the
+// split-KV calls below keep the same limit).
 extern "C" int fav4_bshd_forward_gqa(const Fav4Args* args, int kv_heads, int causal, int config,
                                      hipStream_t stream);
 
@@ -144,9 +146,12 @@ extern "C" int fav4_bshd_forward_varlen(const Fav4VarlenArgs* args, int causal, 
 // causal = 2 (these calls and the paged ones only): bottom-right causal,
 // query i of a sequence with sq queries and sk keys sees keys j <= sk - sq + i
 // (the last query sees them all; with sq > sk the first sq - sk rows see
-// none: O = 0, LSE = -inf).  It is planned like a dense call (max_seqlen_q >
-// 32: the contiguous prefill plan at the max lengths, 8-wave kernels) and
-// always runs the split kernels, one chunk included (with a workspace).  Same argument contract
+// none: O = 0, LSE = -inf).  Decode (max_seqlen_q <= 32) is planned like a
+// dense call; prefill (max_seqlen_q > 32, 8-wave kernels) with the contiguous
+// prefill plan at the max lengths, counting for each 256-row q tile only the
+// keys up to its last row's diagonal (chunks past it are empty and end at
+// once).  It always runs the split kernels, one chunk included (with a
+// workspace).  Same argument contract
 // as fav4_bshd_forward_varlen (O and LSE rows, empty sequences, offset
 // clamping), plus:
 //  * splits: 0 = library choice (the chunk size the contiguous split-KV Auto

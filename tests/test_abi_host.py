@@ -102,9 +102,31 @@ def test_rejects_bad_arguments(lib, Args, name, change):
     fields.update(change)
     a = Args(**fields)
     assert lib.fav4_bshd_forward(C.byref(a), 0, 0, None) == HIP_ERROR_INVALID_VALUE
-    # the split-KV and GQA entry points apply the same checks first
+    # the split-KV and GQA entry points apply the same checks first (GQA with
+    # kv_heads = heads: the MHA limits)
     assert lib.fav4_bshd_forward_splitkv(C.byref(a), 0, 4, 0x100000, 1 << 30, None) == HIP_ERROR_INVALID_VALUE
-    assert lib.fav4_bshd_forward_gqa(C.byref(a), 1, 0, 0, None) == HIP_ERROR_INVALID_VALUE
+    assert lib.fav4_bshd_forward_gqa(C.byref(a), max(a.heads, 1), 0, 0, None) == HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.parametrize("sk", [131072, 200000, (1 << 31) // (8 * 128) - 1])
+def test_gqa_key_limit_counts_kv_heads(lib, Args, sk):
+    """H128 with 8 K/V heads: the key-side limit is sk * kv_heads * 128 < 2^31
+    (K/V rows are kv_heads * 256 bytes apart), so long caches are accepted by
+    the split-KV queries, for prefill and decode shapes alike, while the MHA
+    form of the same shape (kv_heads = heads) is rejected."""
+    for sq in (1, 4096):
+        fields = _good(Args)
+        fields.update(batch=1, heads=128, sq=sq, sk=sk)
+        a = Args(**fields)
+        splits = lib.fav4_bshd_splitkv_gqa_select(C.byref(a), 8, 0)
+        assert splits >= 1, (sq, sk, splits)
+        ws = lib.fav4_bshd_splitkv_gqa_workspace_size(C.byref(a), 8, 0, 0)
+        assert ws == (0 if splits == 1 else splits * 128 * sq * (128 * 4 + 8)), (sq, sk, ws)
+        assert lib.fav4_bshd_splitkv_gqa_select(C.byref(a), 128, 0) == -1
+        assert lib.fav4_bshd_splitkv_gqa_workspace_size(C.byref(a), 128, 0, 0) == -1
+    # one past the limit is rejected with 8 K/V heads too
+    fields.update(sk=(1 << 31) // (8 * 128))
+    assert lib.fav4_bshd_splitkv_gqa_select(C.byref(Args(**fields)), 8, 0) == -1
 
 
 @pytest.mark.parametrize("causal,config", [(-1, 0), (2, 0), (0, -1), (0, 4), (1, 7)])
