@@ -60,7 +60,9 @@ def parse_args():
     p.add_argument("--no-check", action="store_true", help="skip the sampled-row FP64 check")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
-    p.add_argument("--sweep", default="", help="comma list of extra sequence lengths to time (report only)")
+    p.add_argument("--sweep", default="512,1024,8192,16384,32768",
+                   help="comma list of the long-sequence sweep's lengths (B and H as the headline; dense and causal)")
+    p.add_argument("--no-sweep", action="store_true", help="skip the long-sequence sweep")
     p.add_argument("--no-comparator", action="store_true", help="skip the torch SDPA comparator")
     p.add_argument("--no-splitkv", action="store_true", help="skip the split-KV report (B1 H8 Sq1024 Sk32768; B1 H1 S16384 causal)")
     p.add_argument("--no-api", action="store_true", help="skip the GQA / varlen report")
@@ -106,15 +108,18 @@ def bits(torch, t):
 
 
 def check_rows(torch, orc, q, k, v, o, causal, pairs):
-    """FP64 oracle on the reference's sampled rows for the given (b, h) pairs."""
+    """FP64 oracle on the reference's sampled rows for the given (b, h) pairs.
+    Only those slices are copied to the host (a full S32768 tensor is 2 GiB)."""
     s = q.shape[1]
     rows = orc.sample_rows(s)
-    qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
-    ref, _ = orc.attention_fp64(qb, kb, vb, orc.DEFAULT_SCALE, causal, rows=rows, heads=pairs)
-    got = bits(torch, o[:, rows])
-    sel_ref = np.stack([ref[b, :, h] for b, h in pairs])
-    sel_got = np.stack([got[b, :, h] for b, h in pairs])
-    return orc.errors(sel_got, None, sel_ref, None), rows
+    rows_t = torch.from_numpy(rows).to(q.device)
+    refs, gots = [], []
+    for b, h in pairs:
+        sl = lambda t: bits(torch, t[b:b + 1, :, h:h + 1])
+        ref, _ = orc.attention_fp64(sl(q), sl(k), sl(v), orc.DEFAULT_SCALE, causal, rows=rows)
+        refs.append(ref[0, :, 0])
+        gots.append(bits(torch, o[b:b + 1].index_select(1, rows_t)[:, :, h:h + 1])[0, :, 0])
+    return orc.errors(np.stack(gots), None, np.stack(refs), None), rows
 
 
 def time_graph(torch, fn, steps, warmup, observations, stream, spin_ms=0.0):
@@ -156,18 +161,36 @@ def time_graph(torch, fn, steps, warmup, observations, stream, spin_ms=0.0):
 
 
 def cpu_info():
-    """(model name, socket count) of the host CPU from /proc/cpuinfo."""
-    model, sockets = "unknown", set()
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name") and model == "unknown":
-                    model = line.split(":", 1)[1].strip()
-                elif line.startswith("physical id"):
-                    sockets.add(line.split(":", 1)[1].strip())
-    except OSError:
-        pass
-    return model, max(1, len(sockets))
+    """Host CPU description: lscpu's model name (else /proc/cpuinfo's), sockets,
+    and the cores this process may run on."""
+    info = {"model": None, "sockets": None, "affinity_cores": len(os.sched_getaffinity(0))}
+    txt = _run(["lscpu"], force=True)
+    for ln in (txt or "").splitlines():
+        key, _, val = ln.partition(":")
+        key, val = key.strip(), val.strip()
+        if key == "Model name" and not info["model"]:
+            info["model"] = val
+        elif key == "BIOS Model name":
+            info["bios_model"] = val
+        elif key == "Socket(s)":
+            info["sockets"] = int(val) if val.isdigit() else val
+    if not info["model"]:
+        try:
+            with open("/proc/cpuinfo") as f:
+                info["model"] = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
+                                     None)
+        except OSError:
+            pass
+    return info
+
+
+def cpu_threads():
+    """Worker threads for the CPU baseline: every core of this process's
+    affinity set, capped by OMP_NUM_THREADS when the launcher sets it (the
+    CPU share granted beside one GPU, 16 on the MI355X boxes used here)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return (min(n, int(cap)) if cap.isdigit() and int(cap) > 0 else n), n
 
 
 def _attention_fp32_slice(qb, kb, vb, bh, scale):
@@ -190,7 +213,7 @@ def cpu_baseline(torch, orc, q, k, v, budget_s):
     from concurrent.futures import ThreadPoolExecutor
     from threadpoolctl import threadpool_limits
     b, s, h, d = q.shape
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores, affinity = cpu_threads()
     qb, kb, vb = bits(torch, q), bits(torch, k), bits(torch, v)
     pairs = [(i, j) for i in range(b) for j in range(h)]
 
@@ -207,15 +230,17 @@ def cpu_baseline(torch, orc, q, k, v, budget_s):
     done, elapsed = run(lambda p: orc.attention_fp64(qb, kb, vb, orc.DEFAULT_SCALE, False, heads=[p]), budget_s)
     done32, elapsed32 = run(lambda p: _attention_fp32_slice(qb, kb, vb, p, orc.DEFAULT_SCALE), budget_s / 2)
     flop1 = orc.flops(1, 1, s, s, False)
-    model, sockets = cpu_info()
+    host = cpu_info()
     return dict(value=flop1 * done / elapsed / 1e12, unit="TFLOP/s", cores=cores, kind="port",
                 sample=f"FP64 numpy oracle, {done} of {len(pairs)} (b,h) slices of B{b} H{h} "
                        f"S{s} D{d} dense, {elapsed:.1f} s on {cores} threads (one slice per thread, "
-                       f"single-threaded BLAS); extrapolated whole-job time "
-                       f"{elapsed * len(pairs) / done:.1f} s",
+                       f"single-threaded BLAS; {affinity} cores in the affinity set, threads capped by "
+                       f"OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'unset')}); extrapolated "
+                       f"whole-job time {elapsed * len(pairs) / done:.1f} s",
                 fp32=dict(value=round(flop1 * done32 / elapsed32 / 1e12, 4), unit="TFLOP/s",
                           sample=f"FP32 numpy textbook attention, {done32} slices in {elapsed32:.1f} s"),
-                cpu_model=model, sockets=sockets)
+                cpu_model=host.get("model"), bios_model=host.get("bios_model"), sockets=host.get("sockets"),
+                affinity_cores=affinity)
 
 
 def time_eager(torch, fn, steps, warmup, stream):
@@ -500,9 +525,9 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
 _TELEMETRY = True
 
 
-def _run(cmd, timeout=20):
+def _run(cmd, timeout=20, force=False):
     import subprocess
-    if not _TELEMETRY:
+    if not (_TELEMETRY or force):
         return None
     try:
         r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
@@ -527,6 +552,57 @@ def gpu_clocks():
             except ValueError:
                 pass
     return {d: c for d, c in clocks.items() if d.startswith(("GFX", "MEM"))} or None
+
+
+def gpu_telemetry():
+    """One amd-smi snapshot: GFX clock (mean / min / max over the XCDs, MHz),
+    memory clock, power, temperatures and activity, or None."""
+    txt = _run(["amd-smi", "metric", "-c", "-p", "-t", "-u", "--json"])
+    if not txt:
+        return None
+    try:
+        start = min(i for i in (txt.find("{"), txt.find("[")) if i >= 0)
+        doc = json.loads(txt[start:])
+    except ValueError:
+        return None
+    gpus = doc.get("gpu_data", doc) if isinstance(doc, dict) else doc
+    if not isinstance(gpus, list) or not gpus or not isinstance(gpus[0], dict):
+        return None
+    g = gpus[0]
+    out = {}
+    clk = g.get("clock") or {}
+    gfx = [d["clk"]["value"] for n, d in clk.items()
+           if n.lower().startswith("gfx") and isinstance(d, dict) and isinstance(d.get("clk"), dict)
+           and isinstance(d["clk"].get("value"), (int, float))]
+    if gfx:
+        out["gfx_mhz"] = dict(mean=round(statistics.mean(gfx)), min=min(gfx), max=max(gfx))
+    mem = (clk.get("mem_0") or {}).get("clk") if isinstance(clk.get("mem_0"), dict) else None
+    if isinstance(mem, dict) and isinstance(mem.get("value"), (int, float)):
+        out["mem_mhz"] = mem["value"]
+
+    def flat(x, path, sink):
+        if isinstance(x, dict):
+            if isinstance(x.get("value"), (int, float)):
+                sink[path] = x["value"]
+                return
+            for key, val in x.items():
+                flat(val, f"{path}.{key}" if path else key, sink)
+        elif isinstance(x, (int, float)) and not isinstance(x, bool):
+            sink[path] = x
+
+    for sec in ("power", "temperature", "usage"):
+        sink = {}
+        flat(g.get(sec), "", sink)
+        if sink:
+            out[sec] = sink
+    return out or None
+
+
+def timed_with_telemetry(fn):
+    """(fn(), amd-smi snapshots before and after it)."""
+    before = gpu_telemetry()
+    res = fn()
+    return res, {"before": before, "after": gpu_telemetry()}
 
 
 def loaded_gfx_clock(torch, fn, stream, launches=200, reps=4):
@@ -562,20 +638,67 @@ def provenance(torch, lib_path):
         digest.update(p.read_bytes())
     hipcc = _run(["hipcc", "--version"])
     prop = torch.cuda.get_device_properties(0)
-    return {"library": str(Path(lib_path).relative_to(ROOT)), "library_sha256": h(lib_path),
+    lib_sha = h(lib_path)
+    manifest = None
+    mpath = Path(lib_path).parent / "build-manifest.json"
+    if mpath.exists():
+        try:
+            manifest = json.loads(mpath.read_text())
+        except ValueError:
+            manifest = {"error": "unreadable build-manifest.json"}
+    lib_entry = ((manifest or {}).get("libraries") or {}).get(Path(lib_path).name) or {}
+    return {"library": str(Path(lib_path).relative_to(ROOT)), "library_sha256": lib_sha,
             "sources_sha256": digest.hexdigest(),
+            "build_manifest": manifest,
+            "library_matches_manifest": (lib_entry.get("sha256") == lib_sha) if lib_entry else None,
             "hipcc": next((ln for ln in (hipcc or "").splitlines() if "HIP version" in ln), None),
             "torch": torch.__version__, "device": f"{prop.name} {prop.gcnArchName} {prop.multi_processor_count} CUs",
             "clocks_before": gpu_clocks()}
 
 
-def read_traffic():
+def read_traffic(lib_sha):
+    """HBM bytes per dense headline launch from the committed counter summary,
+    and whether those counters were taken on the library being timed."""
     if not TRAFFIC_FILE.exists():
-        return None
+        return None, None, None
+    traffic = counters_sha = None
     for line in TRAFFIC_FILE.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
-            return int(float(line.split(":", 1)[1]))
-    return None
+            traffic = int(float(line.split(":", 1)[1]))
+        elif line.startswith("library_sha256:"):
+            counters_sha = line.split(":", 1)[1].strip()
+    return traffic, counters_sha, (counters_sha != lib_sha)
+
+
+def headline(torch, orc, runner, args, b, h, s, stream, pairs, spin_ms=0.0, observations=None):
+    """Sampled-row check, then graph timing of the dense and causal forward at
+    B{b} H{h} S{s}, each with amd-smi snapshots around its timed region."""
+    q, k, v = make_inputs(torch, b, h, s)
+    o = torch.empty_like(q)
+    out = {}
+    for causal in ([False] if args.no_causal else [False, True]):
+        fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
+        check = None
+        if not args.no_check:
+            o.fill_(float("nan"))
+            torch.cuda.synchronize()   # the fill runs on the default stream
+            with torch.cuda.stream(stream):
+                fn()
+            torch.cuda.synchronize()
+            check, _ = check_rows(torch, orc, q, k, v, o, causal, pairs)
+            if not orc.check_acceptance_tolerance(check):
+                raise SystemExit(f"sampled-row check failed (B{b} H{h} S{s} causal={causal}): {check}")
+        samples, tel = timed_with_telemetry(
+            lambda: time_graph(torch, fn, args.steps, args.warmup, observations or args.observations, stream,
+                               spin_ms=spin_ms))
+        flop = orc.flops(b, h, s, s, causal)
+        us = statistics.mean(samples)
+        out[causal] = dict(us=us, median_us=statistics.median(samples), samples_us=samples,
+                           tflops=flop / us / 1e6, flop=flop, check=check, telemetry=tel)
+        print(f"# B{b} H{h} S{s} causal={causal}: {us:.1f} us/launch, {flop / us / 1e6:.1f} TFLOP/s "
+              f"({flop / us / 1e6 / PEAK_BF16_TFLOPS * 100:.1f}% of peak) check={check}",
+              file=sys.stderr, flush=True)
+    return out, (q, k, v, o)
 
 
 def main():
@@ -597,80 +720,48 @@ def main():
 
     b, h, s = args.batch, args.heads, args.seq
     prov = provenance(torch, pkg.LIB_PATH)
-    q, k, v = make_inputs(torch, b, h, s)
-    o = torch.empty_like(q)
     stream = torch.cuda.Stream()
     pairs = [(0, 0), (b // 2, h // 2), (b - 1, h - 1)]
-    results = {}
-    for causal in ([False] if args.no_causal else [False, True]):
-        fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
-        check = None
-        if not args.no_check:
-            o.fill_(float("nan"))
-            torch.cuda.synchronize()   # the fill runs on the default stream
-            with torch.cuda.stream(stream):
-                fn()
-            torch.cuda.synchronize()
-            check, _ = check_rows(torch, orc, q, k, v, o, causal, pairs)
-            if not orc.check_acceptance_tolerance(check):
-                raise SystemExit(f"sampled-row check failed (causal={causal}): {check}")
-        samples = time_graph(torch, fn, args.steps, args.warmup, args.observations, stream)
-        flop = orc.flops(b, h, s, s, causal)
-        us = statistics.mean(samples)
-        results[causal] = dict(us=us, median_us=statistics.median(samples), samples_us=samples,
-                               tflops=flop / us / 1e6, flop=flop, check=check)
-        print(f"# B{b} H{h} S{s} causal={causal}: {us:.1f} us/launch, {flop / us / 1e6:.1f} TFLOP/s "
-              f"({flop / us / 1e6 / PEAK_BF16_TFLOPS * 100:.1f}% of peak) check={check}",
-              file=sys.stderr, flush=True)
+    results, (q, k, v, o) = headline(torch, orc, runner, args, b, h, s, stream, pairs)
+    dense = results[False]
+    clk = loaded_gfx_clock(torch, lambda: runner.call(q, k, v, o, None, False, args.config,
+                                                      stream=stream.cuda_stream), stream) if _TELEMETRY else None
+    # The CPU baseline times the oracle on slices of the same dense inputs.
+    cpu = None if args.no_cpu_baseline else cpu_baseline(torch, orc, q, k, v, args.cpu_seconds)
 
     cmp = None
     if not args.no_comparator:
         cmp = comparator(torch, orc, runner, q, k, v, o, stream, args, list(results))
+    del q, k, v, o
+    torch.cuda.empty_cache()
     skv = None if args.no_splitkv else splitkv_report(torch, orc, runner, args, stream)
     api = None if args.no_api else api_report(torch, orc, runner, args, stream)
 
+    # Long-sequence sweep (B and H of the headline): each shape checked on
+    # sampled rows, then graph-timed (2 observations) after an untimed spin-up.
     sweep = {}
-    for n in [int(x) for x in args.sweep.split(",") if x]:
-        del q, k, v, o
+    for n in ([] if args.no_sweep else [int(x) for x in args.sweep.split(",") if x]):
+        res, bufs = headline(torch, orc, runner, args, b, h, n, stream, pairs, spin_ms=SWEEP_SPIN_MS,
+                             observations=2)
+        del bufs
         torch.cuda.empty_cache()
-        q, k, v = make_inputs(torch, b, h, n)
-        o = torch.empty_like(q)
-        for causal in (False, True):
-            fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
-            check = None
-            if not args.no_check:
-                o.fill_(float("nan"))
-                torch.cuda.synchronize()
-                with torch.cuda.stream(stream):
-                    fn()
-                torch.cuda.synchronize()
-                check, _ = check_rows(torch, orc, q, k, v, o, causal, pairs)
-                if not orc.check_acceptance_tolerance(check):
-                    raise SystemExit(f"sampled-row check failed (S{n}, causal={causal}): {check}")
-            sm = time_graph(torch, fn, args.steps, args.warmup, 2, stream, spin_ms=SWEEP_SPIN_MS)
-            us = statistics.mean(sm)
-            tf = orc.flops(b, h, n, n, causal) / us / 1e6
-            sweep[f"S{n}_{'causal' if causal else 'dense'}"] = dict(us=round(us, 2), tflops=round(tf, 1),
-                                                                    check=check)
-            print(f"# sweep S{n} causal={causal}: {us:.1f} us, {tf:.1f} TFLOP/s check={check}", file=sys.stderr,
-                  flush=True)
+        for causal, r in res.items():
+            sweep[f"S{n}_{'causal' if causal else 'dense'}"] = dict(
+                us=round(r["us"], 2), tflops=round(r["tflops"], 1),
+                frac_of_peak=round(r["tflops"] / PEAK_BF16_TFLOPS, 4), check=r["check"],
+                telemetry=r["telemetry"])
 
-    dense = results[False]
-    clk = loaded_gfx_clock(torch, lambda: runner.call(q, k, v, o, None, False, args.config,
-                                                      stream=stream.cuda_stream), stream) if _TELEMETRY else None
-    traffic = read_traffic()
+    traffic, counters_sha, stale = read_traffic(prov["library_sha256"])
     compulsory = 2 * b * h * 128 * (2 * s + 2 * s)
     roofline = dict(bound="mfma", achieved=round(dense["tflops"], 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
                     frac=round(dense["tflops"] / PEAK_BF16_TFLOPS, 4), traffic=traffic,
+                    traffic_library_sha256=counters_sha, traffic_stale=stale,
                     kernel="fav4::fwd_kernel (dense)", flop_per_launch=dense["flop"],
                     avg_launch_us=round(dense["us"], 3), compulsory_hbm_bytes=compulsory,
                     hbm_roofline_tflops=round(dense["flop"] / compulsory * HBM_TBPS, 1),
                     gfx_clock_mhz_under_load=clk,
                     peak_at_loaded_clock=round(PEAK_BF16_TFLOPS * clk / 2400, 1) if clk else None,
                     frac_at_loaded_clock=round(dense["tflops"] / (PEAK_BF16_TFLOPS * clk / 2400), 4) if clk else None)
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline(torch, orc, q, k, v, args.cpu_seconds) if not sweep else None
     line = {
         "metric": "fwd TFLOP/s + % BF16 MFMA peak, B32 H8 D128 S4096 dense & causal",
         "value": round(dense["tflops"], 2),
@@ -697,12 +788,14 @@ def main():
         line["causal"] = dict(value=round(c["tflops"], 2), unit="TFLOP/s", us_per_launch=round(c["us"], 3),
                               median_us_per_launch=round(c["median_us"], 3),
                               frac_of_peak=round(c["tflops"] / PEAK_BF16_TFLOPS, 4),
-                              samples_us=[round(x, 2) for x in c["samples_us"]])
+                              samples_us=[round(x, 2) for x in c["samples_us"]], telemetry=c["telemetry"])
     line["dense_samples_us"] = [round(x, 2) for x in dense["samples_us"]]
+    line["dense_telemetry"] = dense["telemetry"]
     line["comparator"] = cmp
     line["splitkv"] = skv
     line["api"] = api
     prov["clocks_after"] = gpu_clocks()
+    prov["host_cpu"] = cpu_info()
     line["provenance"] = prov
     if sweep:
         line["sweep"] = sweep

@@ -93,6 +93,64 @@ struct LdsOffsets {
     uint32_t v[2][4];   // V^T operand: [first/second 4-key group][32-dim block]
 };
 
+// MFMA operand read offsets of one lane.  K (A operand of S^T = K.Q^T, one
+// 32-key block): lane l reads key l % 32, dims 16c + 8(l / 32) .. +7, i.e.
+// granule 2c + l / 32 of its row, found at that granule ^ k_swz(row).  V^T
+// (A operand of O^T += V^T.P^T, one 16-key unit): ds_read_b64_tr_b16 from
+// lane l returns dim l % 32 of a 32-dim block for four keys, so source lane
+// 4r + c of each 16-lane group addresses row r (+ 4 for the upper lane half,
+// + 8 for the second read) and 4 dims 4c.. of the block.
+__device__ __forceinline__ LdsOffsets lds_offsets(int lane) {
+    const int col = lane & 31, half = lane >> 5;
+    LdsOffsets off;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) off.k[c] = col * ROW_BYTES + ((((2 * c) | half) ^ k_swz(col)) << 4);
+    const int r0 = half * 4 + ((lane & 15) >> 2);             // row inside a 16-key sub-block
+    const int gl = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);  // granule inside a 32-dim block
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r = r0 + 8 * j;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+            off.v[j][db] = r * ROW_BYTES + (((db * 4 + gl) ^ v_swz(r)) << 4) + ((lane & 1) << 3);
+    }
+    return off;
+}
+
+// Per-lane global source offsets of the tile DMA.  Each wave issues DMA ops
+// i = 0..DMA-1 per matrix; op i covers tile rows 4(wave * DMA + i) .. +3, lane
+// l fetching granule (l % 16) ^ swz(row) of row 4(wave * DMA + i) + l / 16, so
+// that the 1 KiB the op writes contiguously to LDS holds the rows swizzled.
+template <int DMA>
+struct DmaOffsets {
+    uint32_t k[DMA], v[DMA];
+};
+template <int DMA>
+__device__ __forceinline__ DmaOffsets<DMA> dma_offsets(int wave, int lane, uint32_t k_row_bytes,
+                                                       uint32_t v_row_bytes) {
+    DmaOffsets<DMA> d;
+#pragma unroll
+    for (int i = 0; i < DMA; ++i) {
+        const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
+        d.k[i] = r * k_row_bytes + ((p ^ k_swz(r)) << 4);
+        d.v[i] = r * v_row_bytes + ((p ^ v_swz(r)) << 4);
+    }
+    return d;
+}
+
+// DMA of one K and one V tile (descriptors rk / rv start at the tile's first
+// row) into the LDS stage at byte address `stage` (K at +0, V at
+// +TILE_BYTES): this wave's DMA ops land at 1 KiB slots wave * DMA + i.
+template <int DMA, int TILE_BYTES>
+__device__ __forceinline__ void dma_tile(u32x4 rk, u32x4 rv, uint32_t stage, int wave, const DmaOffsets<DMA>& d) {
+    const uint32_t base = stage + wave * DMA * 1024;
+#pragma unroll
+    for (int i = 0; i < DMA; ++i) {
+        dma16(rk, base + i * 1024, d.k[i]);
+        dma16(rv, base + TILE_BYTES + i * 1024, d.v[i]);
+    }
+}
+
 // S^T = K.Q^T for one tile: 8 MFMAs per 32-key block, K operands read ahead.
 // Masked tiles compute every block too (no branch around blocks past the key
 // length or above the diagonal): tile_mask then hides them, and the tile
@@ -324,28 +382,8 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
     const float scale2 = a.scale * LOG2E;
     const uint32_t smem_base = lds_addr(smem);
 
-    LdsOffsets off;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) off.k[c] = col * ROW_BYTES + ((((2 * c) | half) ^ k_swz(col)) << 4);
-    {
-        const int r0 = half * 4 + ((lane & 15) >> 2);             // row inside a 16-key sub-block
-        const int gl = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);  // granule inside a 32-dim block
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int r = r0 + 8 * j;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-                off.v[j][db] = r * ROW_BYTES + (((db * 4 + gl) ^ v_swz(r)) << 4) + ((lane & 1) << 3);
-        }
-    }
-    // Per-lane DMA source offsets inside a tile: each op covers 4 rows x 16 granules.
-    uint32_t dk[DMA], dv[DMA];
-#pragma unroll
-    for (int i = 0; i < DMA; ++i) {
-        const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
-        dk[i] = r * L.kr + ((p ^ k_swz(r)) << 4);
-        dv[i] = r * L.vr + ((p ^ v_swz(r)) << 4);
-    }
+    const LdsOffsets off = lds_offsets(lane);
+    const DmaOffsets<DMA> dofs = dma_offsets<DMA>(wave, lane, L.kr, L.vr);
 
     auto process = [&](int bh, int tile) {
         const int batch = bh / a.heads, head = bh - batch * a.heads;
@@ -374,12 +412,7 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
             const uint32_t rows = uint32_t(a.sk - int(first) - 1);
             const u32x4 rk = make_desc(kbase + first * L.kr, rows * L.kr + ROW_BYTES);
             const u32x4 rv = make_desc(vbase + first * L.vr, rows * L.vr + ROW_BYTES);
-            const uint32_t ks = smem_base + (t % STAGES) * STAGE_BYTES + wave * DMA * 1024;
-#pragma unroll
-            for (int i = 0; i < DMA; ++i) {
-                dma16(rk, ks + i * 1024, dk[i]);
-                dma16(rv, ks + TILE_BYTES + i * 1024, dv[i]);
-            }
+            dma_tile<DMA, TILE_BYTES>(rk, rv, smem_base + (t % STAGES) * STAGE_BYTES, wave, dofs);
         };
 
 #pragma unroll
@@ -667,27 +700,8 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
     const uint32_t smem_base = lds_addr(smem);
     const int bhs = a.batch * a.heads;
 
-    LdsOffsets off;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) off.k[c] = col * ROW_BYTES + ((((2 * c) | half) ^ k_swz(col)) << 4);
-    {
-        const int r0 = half * 4 + ((lane & 15) >> 2);
-        const int gl = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int r = r0 + 8 * j;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-                off.v[j][db] = r * ROW_BYTES + (((db * 4 + gl) ^ v_swz(r)) << 4) + ((lane & 1) << 3);
-        }
-    }
-    uint32_t dk[DMA], dv[DMA];
-#pragma unroll
-    for (int i = 0; i < DMA; ++i) {
-        const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
-        dk[i] = r * kv_row_bytes + ((p ^ k_swz(r)) << 4);
-        dv[i] = r * kv_row_bytes + ((p ^ v_swz(r)) << 4);
-    }
+    const LdsOffsets off = lds_offsets(lane);
+    const DmaOffsets<DMA> dofs = dma_offsets<DMA>(wave, lane, kv_row_bytes, kv_row_bytes);
 
     // Rows of one item's row space: a head's queries, or a group's.
     const int rows = PACK ? group * a.sq : a.sq;
@@ -777,12 +791,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
                 const uint32_t bytes = uint32_t(rows_left - 1) * kv_row_bytes + ROW_BYTES;
                 const u32x4 rk = make_desc(kbase + row0 * kv_row_bytes, bytes);
                 const u32x4 rv = make_desc(vbase + row0 * kv_row_bytes, bytes);
-                const uint32_t ks = smem_base + ((t - t0) % STAGES) * STAGE_BYTES + wave * DMA * 1024;
-#pragma unroll
-                for (int i = 0; i < DMA; ++i) {
-                    dma16(rk, ks + i * 1024, dk[i]);
-                    dma16(rv, ks + TILE_BYTES + i * 1024, dv[i]);
-                }
+                dma_tile<DMA, TILE_BYTES>(rk, rv, smem_base + ((t - t0) % STAGES) * STAGE_BYTES, wave, dofs);
             };
             issue(t0);
             issue(t0 + 1);
@@ -889,27 +898,8 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
     const float scale2 = a.scale * LOG2E;
     const uint32_t smem_base = lds_addr(smem);
 
-    LdsOffsets off;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) off.k[c] = col * ROW_BYTES + ((((2 * c) | half) ^ k_swz(col)) << 4);
-    {
-        const int r0 = half * 4 + ((lane & 15) >> 2);
-        const int gl = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int r = r0 + 8 * j;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-                off.v[j][db] = r * ROW_BYTES + (((db * 4 + gl) ^ v_swz(r)) << 4) + ((lane & 1) << 3);
-        }
-    }
-    uint32_t dk[DMA], dv[DMA];
-#pragma unroll
-    for (int i = 0; i < DMA; ++i) {
-        const int r = (wave * DMA + i) * 4 + (lane >> 4), p = lane & 15;
-        dk[i] = r * kv_row_bytes + ((p ^ k_swz(r)) << 4);
-        dv[i] = r * kv_row_bytes + ((p ^ v_swz(r)) << 4);
-    }
+    const LdsOffsets off = lds_offsets(lane);
+    const DmaOffsets<DMA> dofs = dma_offsets<DMA>(wave, lane, kv_row_bytes, kv_row_bytes);
 
     // Item order.  Each XCD gets a contiguous run of logical items (all q
     // tiles of a (sequence, head) together, for its L2), but the runs are cut
@@ -968,12 +958,7 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
                 const uint32_t bytes = uint32_t(sk - int(first) - 1) * kv_row_bytes + ROW_BYTES;
                 const u32x4 rk = make_desc(kbase + first * kv_row_bytes, bytes);
                 const u32x4 rv = make_desc(vbase + first * kv_row_bytes, bytes);
-                const uint32_t kd = smem_base + (t & 1) * STAGE_BYTES + wave * DMA * 1024;
-#pragma unroll
-                for (int i = 0; i < DMA; ++i) {
-                    dma16(rk, kd + i * 1024, dk[i]);
-                    dma16(rv, kd + TILE_BYTES + i * 1024, dv[i]);
-                }
+                dma_tile<DMA, TILE_BYTES>(rk, rv, smem_base + (t & 1) * STAGE_BYTES, wave, dofs);
             };
             issue(0);
             bf16x8 qr[8];

@@ -28,8 +28,13 @@ HIPCC_FLAGS = [
     "-fgpu-flush-denormals-to-zero",
     # keep the compiler from emitting packed-FP32 VALU ops (v_pk_fma_f32 & co.)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # per-kernel VGPR / AGPR / SGPR counts, spills, LDS and occupancy, as
+    # compiler remarks (the reference's scripts/build.sh:14-17 keeps the same)
+    "-Rpass-analysis=kernel-resource-usage",
 ]
-
+KAT_LIB_PATH = ROOT / "build" / "libfav4_loader_kat.so"
+RESOURCE_LOG = ROOT / "build" / "resource-usage.txt"
+MANIFEST = ROOT / "build" / "build-manifest.json"
 
 class Args(C.Structure):
     """``struct Fav4Args`` (include/fav4_bshd.h): 5 pointers, 4 ints, 1 float."""
@@ -57,18 +62,66 @@ class Strides(C.Structure):
     _fields_ = [(n, C.c_longlong) for n in ("batch", "seq", "head")]
 
 
+def parse_resource_usage(text: str) -> dict:
+    """Per-kernel fields of hipcc's kernel-resource-usage remarks."""
+    table, name = {}, None
+    for line in text.splitlines():
+        if "remark:" not in line or "kernel-resource-usage" not in line:
+            continue
+        body = line.split("remark:", 1)[1].rsplit("[-Rpass-analysis", 1)[0].strip()
+        key, _, val = body.partition(":")
+        key, val = key.strip(), val.strip()
+        if key == "Function Name":
+            name = val
+            table[name] = {}
+        elif name is not None:
+            table[name][key] = int(val) if val.lstrip("-").isdigit() else val
+    return table
+
+
 def build_library(out: Path = LIB_PATH, verbose: bool = False) -> Path:
-    """Compile ``csrc/bshd.hip`` for gfx950 into ``build/libfav4_bshd.so``."""
+    """Compile ``csrc/bshd.hip`` for gfx950 into ``build/libfav4_bshd.so`` and
+    the loader probe ``csrc/loader_kat.hip`` into ``build/libfav4_loader_kat.so``
+    (a test library), keep the compiler's kernel-resource-usage remarks in
+    ``build/resource-usage.txt`` and write ``build/build-manifest.json``
+    (toolchain, flags, source and library sha256, per-kernel resources)."""
+    import hashlib
+    import json
+    import platform
+    import time
     out.parent.mkdir(parents=True, exist_ok=True)
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = out.with_suffix(".so.tmp")
-    cmd = [hipcc, *HIPCC_FLAGS, str(CSRC / "bshd.hip"), "-o", str(tmp)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
-    if verbose and res.stderr:
-        print(res.stderr)
-    os.replace(tmp, out)
+    jobs = {out: CSRC / "bshd.hip", KAT_LIB_PATH: CSRC / "loader_kat.hip"}
+    procs = {}
+    for lib, src in jobs.items():
+        tmp = lib.with_suffix(".so.tmp")
+        procs[lib] = (tmp, subprocess.Popen([hipcc, *HIPCC_FLAGS, str(src), "-o", str(tmp)],
+                                            stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
+    remarks = []
+    for lib, (tmp, proc) in procs.items():
+        _, err = proc.communicate()
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({proc.returncode}) on {jobs[lib].name}:\n{err[-4000:]}")
+        if verbose and err:
+            print(err)
+        remarks.append(err)
+        os.replace(tmp, lib)
+    text = "\n".join(remarks)
+    RESOURCE_LOG.write_text(text)
+    sha = lambda p: hashlib.sha256(Path(p).read_bytes()).hexdigest()
+    version = subprocess.run([hipcc, "--version"], capture_output=True, text=True).stdout
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.hpp")) + [INCLUDE / "fav4_bshd.h"]
+    manifest = {
+        "built_at": time.strftime("%Y-%m-%dT%H:%M:%SZ", time.gmtime()),
+        "host": platform.node(),
+        "hipcc": hipcc, "hipcc_version": [ln for ln in version.splitlines() if ln.strip()][:3],
+        "flags": HIPCC_FLAGS,
+        "sources": {str(p.relative_to(ROOT)): sha(p) for p in sources},
+        "libraries": {lib.name: {"sha256": sha(lib), "bytes": lib.stat().st_size, "source": jobs[lib].name}
+                      for lib in jobs},
+        "kernel_resources": parse_resource_usage(text),
+    }
+    MANIFEST.write_text(json.dumps(manifest, indent=1))
     return out
 
 
