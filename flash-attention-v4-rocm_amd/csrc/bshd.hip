@@ -682,3 +682,53 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_
                ? launch_split<true, true, true, true>(paged_shape(*a), a->kv_heads, p, workspace, sp, stream)
                : launch_split<false, true, true>(paged_shape(*a), a->kv_heads, p, workspace, sp, stream);
 }
+
+// ---- Split-KV without a caller workspace ------------------------------------
+// For callers that cannot allocate (code under HIP graph capture, serving
+// loops, harnesses that forbid it): the chunk partials live in a fixed
+// device-resident array, one copy per GPU, held until the process ends.
+constexpr size_t SCRATCH_BYTES = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+
+namespace {
+
+// Device address of the current device's `scratch` (in host code the array's
+// name is only a stand-in, never a device address), looked up once per device
+// with that device current and kept per device.
+hipError_t scratch_address(void** out) {
+    static std::atomic<void*> cache[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    void* p = cache[dev].load(std::memory_order_acquire);
+    if (!p) {
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        cache[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_gqa_noalloc(const Fav4Args* a,
+                                                                                    int kv_heads, int causal,
+                                                                                    int splits,
+                                                                                    hipStream_t stream) {
+    const int st = split_args_ok(a, kv_heads, causal, splits);
+    if (st != hipSuccess) return st;
+    const SplitPlan p = split_plan(*a, kv_heads, causal, splits);
+    if (p.splits == 1) return fav4_bshd_forward_gqa(a, kv_heads, causal, 0, stream);
+    if (split_workspace(*a, p) > int64_t(SCRATCH_BYTES)) return hipErrorInvalidValue;
+    void* ws = nullptr;
+    const hipError_t e = scratch_address(&ws);
+    if (e != hipSuccess) return e;
+    // Every partial row the merge reads is written by the partial kernel
+    // first, so the array needs no clearing between calls.
+    const fav4::SplitArgs sp{};
+    return causal ? launch_split<true>(*a, kv_heads, p, ws, sp, stream)
+                  : launch_split<false>(*a, kv_heads, p, ws, sp, stream);
+}

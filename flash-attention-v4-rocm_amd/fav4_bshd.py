@@ -153,6 +153,9 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
         lib.fav4_bshd_splitkv_gqa_workspace_size.restype = C.c_longlong
         lib.fav4_bshd_splitkv_gqa_select.argtypes = [C.POINTER(Args), C.c_int, C.c_int]
         lib.fav4_bshd_splitkv_gqa_select.restype = C.c_int
+        lib.fav4_bshd_forward_splitkv_gqa_noalloc.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_int,
+                                                              C.c_void_p]
+        lib.fav4_bshd_forward_splitkv_gqa_noalloc.restype = C.c_int
         lib.fav4_bshd_forward_gqa.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_int, C.c_void_p]
         lib.fav4_bshd_forward_gqa.restype = C.c_int
         lib.fav4_bshd_forward_strided.argtypes = [C.POINTER(Args), C.c_int] + [C.POINTER(Strides)] * 4 + [
@@ -267,6 +270,19 @@ class Runner:
         if status:
             raise RuntimeError(f"splitkv splits {splits}: HIP status {status}")
         return workspace
+
+    def call_splitkv_noalloc(self, q, k, v, o, lse, causal, splits=0, scale=None, stream=None):
+        """fav4_bshd_forward_splitkv_gqa_noalloc: split-KV with the library's own
+        64 MiB per-device partials array (no workspace); K/V heads = k.shape[2]."""
+        import torch
+        kvh = k.shape[2]
+        a = self.args(q, k, v, o, lse, scale, kv_heads=kvh)
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
+        status = self.hip.fav4_bshd_forward_splitkv_gqa_noalloc(C.byref(a), int(kvh), int(causal), int(splits),
+                                                                 stream)
+        if status:
+            raise RuntimeError(f"splitkv noalloc splits {splits}: HIP status {status}")
 
     # ---- arbitrary strides (fav4_bshd_forward_strided; no reference counterpart) ----
     def call_strided(self, q, k, v, o, lse, causal, config=0, scale=None, stream=None):

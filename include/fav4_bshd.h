@@ -92,6 +92,22 @@ extern "C" long long fav4_bshd_splitkv_gqa_workspace_size(const Fav4Args* args, 
                                                           int splits);
 extern "C" int fav4_bshd_splitkv_gqa_select(const Fav4Args* args, int kv_heads, int causal);
 
+// Split-KV with grouped K/V heads and no workspace argument.  No counterpart
+// in the reference: it is for callers that cannot allocate device memory
+// (code under HIP graph capture, tight serving loops, harnesses that forbid
+// hipMalloc).  Exactly fav4_bshd_forward_splitkv_gqa (same checks, plan,
+// kernels and results, bitwise) except that the chunk partials live in a
+// 64 MiB array inside the library, one copy per GPU, held until the process
+// ends.  Plans whose workspace (fav4_bshd_splitkv_gqa_workspace_size) exceeds
+// 64 MiB = 67108864 bytes return hipErrorInvalidValue; splits resolving to 1
+// run fav4_bshd_forward_gqa.  Every call on one GPU shares that GPU's array:
+// calls that overlap on one GPU (other streams, other host threads) race and
+// give undefined results; calls ordered on one stream are safe.  The first
+// call on a device looks the array's address up (hipGetSymbolAddress) and
+// returns that lookup's error if it fails.  Allocates nothing.
+extern "C" int fav4_bshd_forward_splitkv_gqa_noalloc(const Fav4Args* args, int kv_heads, int causal, int splits,
+                                                     hipStream_t stream);
+
 // ---- Grouped-query / multi-query attention ----------------------------------
 // No counterpart in the reference (its README lists GQA as unsupported).  The
 // same contract as fav4_bshd_forward, except that K and V are

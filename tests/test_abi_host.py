@@ -51,7 +51,8 @@ def test_exports_exactly_the_c_abi():
                       "fav4_bshd_splitkv_gqa_workspace_size", "fav4_bshd_splitkv_gqa_select",
                       "fav4_bshd_forward_splitkv_varlen", "fav4_bshd_splitkv_varlen_workspace_size",
                       "fav4_bshd_splitkv_varlen_select", "fav4_bshd_forward_splitkv_paged",
-                      "fav4_bshd_splitkv_paged_workspace_size", "fav4_bshd_splitkv_paged_select"}, public
+                      "fav4_bshd_splitkv_paged_workspace_size", "fav4_bshd_splitkv_paged_select",
+                      "fav4_bshd_forward_splitkv_gqa_noalloc"}, public
 
 
 def test_ctypes_layout_matches_reference(Args):
@@ -669,3 +670,20 @@ def test_strided_applies_forward_checks(lib, Args, name, change):
     a = Args(**f)
     st = [_bshd_strides(2, 256, 4)] * 4
     assert _strided_call(lib, a, max(1, min(4, a.heads if a.heads > 0 else 1)), st) == HIP_ERROR_INVALID_VALUE
+
+
+def test_noalloc_rejects_plans_past_its_array(lib, Args):
+    """The no-workspace split-KV call keeps its partials in a 64 MiB array per
+    device: a plan needing more is rejected before any HIP call, as are the
+    arguments the workspace call rejects."""
+    lib.fav4_bshd_forward_splitkv_gqa_noalloc.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_int, C.c_void_p]
+    fields = _good(Args)
+    fields.update(batch=32, heads=8, sq=4096, sk=32768)
+    a = Args(**fields)
+    need = lib.fav4_bshd_splitkv_gqa_workspace_size(C.byref(a), 8, 0, 8)
+    assert need == 8 * 32 * 8 * 4096 * (128 * 4 + 8) > 64 << 20
+    assert lib.fav4_bshd_forward_splitkv_gqa_noalloc(C.byref(a), 8, 0, 8, None) == HIP_ERROR_INVALID_VALUE
+    for kvh, causal, splits in ((0, 0, 0), (3, 0, 0), (8, 2, 0), (8, 0, 257), (8, 0, -1)):
+        assert lib.fav4_bshd_forward_splitkv_gqa_noalloc(C.byref(a), kvh, causal, splits, None) == \
+            HIP_ERROR_INVALID_VALUE, (kvh, causal, splits)
+    assert lib.fav4_bshd_forward_splitkv_gqa_noalloc(None, 8, 0, 0, None) == HIP_ERROR_INVALID_VALUE
