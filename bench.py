@@ -605,8 +605,11 @@ def timed_with_telemetry(fn):
     return res, {"before": before, "after": gpu_telemetry()}
 
 
-def loaded_gfx_clock(torch, fn, stream, launches=200, reps=4):
-    """Mean GFX clock (MHz) read by amd-smi while a graph of `launches` x fn is replayed back to back."""
+def loaded_telemetry(torch, fn, stream, launches=50, max_s=20.0):
+    """One amd-smi snapshot (clocks, power, temperatures, activity) read from a
+    child process while graphs of `launches` x fn replay back to back; the
+    replays continue until the snapshot is taken (amd-smi's start-up time
+    varies), at most `max_s` seconds."""
     import threading
     with torch.cuda.stream(stream):
         g = torch.cuda.CUDAGraph()
@@ -614,17 +617,18 @@ def loaded_gfx_clock(torch, fn, stream, launches=200, reps=4):
             for _ in range(launches):
                 fn()
     got = {}
-    reader = threading.Thread(target=lambda: (time.sleep(0.3), got.update(c=gpu_clocks())))
+    reader = threading.Thread(target=lambda: (time.sleep(0.3), got.update(t=gpu_telemetry())))
+    t_end = time.perf_counter() + max_s
     with torch.cuda.stream(stream):
         g.replay()
         reader.start()
-        for _ in range(reps - 1):
+        while reader.is_alive() and time.perf_counter() < t_end:
             g.replay()
+            stream.synchronize()
     torch.cuda.synchronize()
     reader.join()
     del g
-    gfx = [v for d, v in (got.get("c") or {}).items() if d.startswith("GFX")]
-    return round(statistics.mean(gfx)) if gfx else None
+    return got.get("t")
 
 
 def provenance(torch, lib_path):
@@ -724,8 +728,14 @@ def main():
     pairs = [(0, 0), (b // 2, h // 2), (b - 1, h - 1)]
     results, (q, k, v, o) = headline(torch, orc, runner, args, b, h, s, stream, pairs)
     dense = results[False]
-    clk = loaded_gfx_clock(torch, lambda: runner.call(q, k, v, o, None, False, args.config,
-                                                      stream=stream.cuda_stream), stream) if _TELEMETRY else None
+    # Clocks, power and temperatures while each headline kernel runs (the
+    # snapshots around the timed regions land when the GPU is already idle).
+    under_load = {}
+    if _TELEMETRY:
+        for causal in results:
+            under_load["causal" if causal else "dense"] = loaded_telemetry(
+                torch, lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream), stream)
+    clk = ((under_load.get("dense") or {}).get("gfx_mhz") or {}).get("mean")
     # The CPU baseline times the oracle on slices of the same dense inputs.
     cpu = None if args.no_cpu_baseline else cpu_baseline(torch, orc, q, k, v, args.cpu_seconds)
 
@@ -759,7 +769,7 @@ def main():
                     kernel="fav4::fwd_kernel (dense)", flop_per_launch=dense["flop"],
                     avg_launch_us=round(dense["us"], 3), compulsory_hbm_bytes=compulsory,
                     hbm_roofline_tflops=round(dense["flop"] / compulsory * HBM_TBPS, 1),
-                    gfx_clock_mhz_under_load=clk,
+                    gfx_clock_mhz_under_load=clk, telemetry_under_load=under_load or None,
                     peak_at_loaded_clock=round(PEAK_BF16_TFLOPS * clk / 2400, 1) if clk else None,
                     frac_at_loaded_clock=round(dense["tflops"] / (PEAK_BF16_TFLOPS * clk / 2400), 4) if clk else None)
     line = {
