@@ -492,6 +492,14 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_select_config(co
     return auto_config(*a, 0);
 }
 
+// The same for a call with this mask (no counterpart in the reference, whose
+// Auto ignores the mask): the config fav4_bshd_forward runs for config 0.
+extern "C" __attribute__((visibility("default"))) int fav4_bshd_select_config_masked(const Fav4Args* a,
+                                                                             int causal) {
+    if (!a || (causal != 0 && causal != 1)) return -1;
+    return auto_config(*a, causal);
+}
+
 // Replaces src/bshd.hip:26-38.
 extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward(const Fav4Args* a, int causal, int config,
                                                                 hipStream_t stream) {

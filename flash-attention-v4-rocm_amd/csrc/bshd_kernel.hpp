@@ -139,16 +139,23 @@ __device__ __forceinline__ DmaOffsets<DMA> dma_offsets(int wave, int lane, uint3
 }
 
 // DMA of one K and one V tile (descriptors rk / rv start at the tile's first
-// row) into the LDS stage at byte address `stage` (K at +0, V at
-// +TILE_BYTES): this wave's DMA ops land at 1 KiB slots wave * DMA + i.
-template <int DMA, int TILE_BYTES>
-__device__ __forceinline__ void dma_tile(u32x4 rk, u32x4 rv, uint32_t stage, int wave, const DmaOffsets<DMA>& d) {
-    const uint32_t base = stage + wave * DMA * 1024;
+// row) to the LDS byte addresses k_lds and v_lds: this wave's DMA ops land at
+// 1 KiB slots wave * DMA + i of each tile.
+template <int DMA>
+__device__ __forceinline__ void dma_kv(u32x4 rk, u32x4 rv, uint32_t k_lds, uint32_t v_lds, int wave,
+                                       const DmaOffsets<DMA>& d) {
+    const uint32_t slot = wave * DMA * 1024;
 #pragma unroll
     for (int i = 0; i < DMA; ++i) {
-        dma16(rk, base + i * 1024, d.k[i]);
-        dma16(rv, base + TILE_BYTES + i * 1024, d.v[i]);
+        dma16(rk, k_lds + slot + i * 1024, d.k[i]);
+        dma16(rv, v_lds + slot + i * 1024, d.v[i]);
     }
+}
+
+// The same into one LDS stage at byte address `stage`: K at +0, V at +TILE_BYTES.
+template <int DMA, int TILE_BYTES>
+__device__ __forceinline__ void dma_tile(u32x4 rk, u32x4 rv, uint32_t stage, int wave, const DmaOffsets<DMA>& d) {
+    dma_kv<DMA>(rk, rv, stage, stage + TILE_BYTES, wave, d);
 }
 
 // S^T = K.Q^T for one tile: 8 MFMAs per 32-key block, K operands read ahead.
@@ -363,6 +370,10 @@ __device__ __forceinline__ void pv_plain(const unsigned char* vs, const LdsOffse
 // each wave always has MFMA and VALU work in flight.  K(t+1) and V(t) are
 // both read between barriers t and t+1; the DMA of tile t+2 goes to the third
 // stage.  Masked tiles (causal diagonal, key tail) follow unpipelined.
+// LDS layout: two stages are [K0 V0 K1 V1]; three are [K0 K1 K2 V0 V1 V2],
+// with the V ring's base folded into the lanes' V offsets once, so that every
+// operand read's constant part stays inside the 16-bit ds_read offset (a
+// stage at 64 KiB or more would otherwise cost an address add per read).
 template <int WAVES, int BN, bool CAUSAL, bool LSE, int STAGES, bool PIPE = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
@@ -382,7 +393,22 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
     const float scale2 = a.scale * LOG2E;
     const uint32_t smem_base = lds_addr(smem);
 
-    const LdsOffsets off = lds_offsets(lane);
+    // K / V tile of stage s: byte offsets from smem, and the pointers the
+    // operand reads use (for three stages the V ring base is in off.v).
+    constexpr auto k_at = [](int s) { return STAGES == 3 ? s * TILE_BYTES : s * STAGE_BYTES; };
+    constexpr auto v_at = [](int s) { return STAGES == 3 ? (3 + s) * TILE_BYTES : s * STAGE_BYTES + TILE_BYTES; };
+    auto kst = [&](int s) -> const unsigned char* { return smem + k_at(s); };
+    auto vst = [&](int s) -> const unsigned char* { return smem + (STAGES == 3 ? s * TILE_BYTES : v_at(s)); };
+    LdsOffsets off = lds_offsets(lane);
+    if constexpr (STAGES == 3) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                off.v[j][db] += 3 * TILE_BYTES;
+                asm volatile("" : "+v"(off.v[j][db]));   // kept whole: not re-split into base + constant
+            }
+    }
     const DmaOffsets<DMA> dofs = dma_offsets<DMA>(wave, lane, L.kr, L.vr);
 
     auto process = [&](int bh, int tile) {
@@ -412,7 +438,8 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
             const uint32_t rows = uint32_t(a.sk - int(first) - 1);
             const u32x4 rk = make_desc(kbase + first * L.kr, rows * L.kr + ROW_BYTES);
             const u32x4 rv = make_desc(vbase + first * L.vr, rows * L.vr + ROW_BYTES);
-            dma_tile<DMA, TILE_BYTES>(rk, rv, smem_base + (t % STAGES) * STAGE_BYTES, wave, dofs);
+            const int s = t % STAGES;
+            dma_kv<DMA>(rk, rv, smem_base + k_at(s), smem_base + v_at(s), wave, dofs);
         };
 
 #pragma unroll
@@ -440,14 +467,13 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
         auto step = [&](auto stage_c, auto masked_c, int t) {
             constexpr int STAGE = decltype(stage_c)::value;
             constexpr bool MASKED = decltype(masked_c)::value;
-            const unsigned char* cur = smem + STAGE * STAGE_BYTES;
             wait_vmem_keep<2 * DMA * (AHEAD - 1)>();
             __syncthreads();
             issue(t + AHEAD);
             // A causal tile entirely above this wave's rows changes nothing
             // (tile 0 never is): the wave only keeps the DMA and barriers.
             if (!(MASKED && CAUSAL) || t * BN <= qw + 31)
-                attend_fused<BN, MASKED, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st, t == 0, t * BN, a.sk,
+                attend_fused<BN, MASKED, CAUSAL, LSE>(kst(STAGE), vst(STAGE), off, qr, st, t == 0, t * BN, a.sk,
                                                       row, half, scale2);
         };
         using S0 = std::integral_constant<int, 0>;
@@ -463,23 +489,21 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
                 SmCarry c;
                 wait_vmem();
                 __syncthreads();
-                tile_qk<BN>(smem, off, qr, sa);
+                tile_qk<BN>(kst(0), off, qr, sa);
                 float mx = tile_rowmax<BN>(sa);
                 // Pipelined tile t (stage STAGE = t%3): S(t) in `cur`, QK^T(t+1)
                 // into `nxt` from stage (t+1)%3, then PV(t).
                 auto pstep = [&](auto stage_c, f32x16 (&cur)[BN / 32], f32x16 (&nxt)[BN / 32], int t) {
                     constexpr int STAGE = decltype(stage_c)::value;
-                    const unsigned char* here = smem + STAGE * STAGE_BYTES;
-                    const unsigned char* ahead = smem + ((STAGE + 1) % 3) * STAGE_BYTES;
                     wait_vmem();        // tile t+1 has landed (issued one tile ago)
                     __syncthreads();
                     issue(t + 2);
                     __builtin_amdgcn_s_setprio(1);
-                    tile_qk<BN>(ahead, off, qr, nxt);
+                    tile_qk<BN>(kst((STAGE + 1) % 3), off, qr, nxt);
                     __builtin_amdgcn_s_setprio(0);
                     softmax_from_max<BN, LSE>(cur, mx, p, st, c, t == 0, scale2);
                     apply_rescale(st, c);
-                    pv_plain<BN>(here + TILE_BYTES, off, p, st);
+                    pv_plain<BN>(vst(STAGE), off, p, st);
                     mx = tile_rowmax<BN>(nxt);
                 };
                 using P0 = std::integral_constant<int, 0>;
@@ -496,7 +520,7 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
                 // Drain tile t (t % 3 == 0): K already consumed, V in stage 0.
                 softmax_from_max<BN, LSE>(sa, mx, p, st, c, t == 0, scale2);
                 apply_rescale(st, c);
-                pv_plain<BN>(smem + TILE_BYTES, off, p, st);
+                pv_plain<BN>(vst(0), off, p, st);
                 ++t;
             }
             // Remaining tiles, unpipelined, prefetch distance 1 (stage t%3).
@@ -505,11 +529,10 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
                 const bool plain = t < nfull;
                 auto mstep = [&](auto stage_c, auto masked_c) {
                     constexpr int STAGE = decltype(stage_c)::value;
-                    const unsigned char* cur = smem + STAGE * STAGE_BYTES;
                     wait_vmem();
                     __syncthreads();
                     issue(t + 1);
-                    attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st,
+                    attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE>(kst(STAGE), vst(STAGE), off, qr, st,
                                                                              t == 0, t * BN, a.sk, row, half,
                                                                              scale2);
                 };

@@ -139,6 +139,8 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
         lib.fav4_bshd_forward.restype = C.c_int
         lib.fav4_bshd_select_config.argtypes = [C.POINTER(Args)]
         lib.fav4_bshd_select_config.restype = C.c_int
+        lib.fav4_bshd_select_config_masked.argtypes = [C.POINTER(Args), C.c_int]
+        lib.fav4_bshd_select_config_masked.restype = C.c_int
         lib.fav4_bshd_forward_splitkv.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_void_p, C.c_size_t,
                                                   C.c_void_p]
         lib.fav4_bshd_forward_splitkv.restype = C.c_int
@@ -219,10 +221,14 @@ class Runner:
         if status:
             raise RuntimeError(f"gqa config {config}: HIP status {status}")
 
-    def select_config(self, q, k) -> int:
+    def select_config(self, q, k, causal=None) -> int:
+        """Config ID that config 0 resolves to: the reference's dense query
+        when `causal` is None, else fav4_bshd_select_config_masked."""
         b, sq, h, _ = q.shape
         a = Args(None, None, None, None, None, b, h, sq, k.shape[1], 1 / math.sqrt(D))
-        return self.hip.fav4_bshd_select_config(C.byref(a))
+        if causal is None:
+            return self.hip.fav4_bshd_select_config(C.byref(a))
+        return self.hip.fav4_bshd_select_config_masked(C.byref(a), int(causal))
 
     # ---- split-KV (fav4_bshd_forward_splitkv; no reference counterpart) ----
     @staticmethod

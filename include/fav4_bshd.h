@@ -41,9 +41,13 @@ struct Fav4Args {
 extern "C" int fav4_bshd_forward(const Fav4Args* args, int causal, int config, hipStream_t stream);
 // Replaces include/fav4_bshd.h:20 (fav4_bshd_select_config): the config ID
 // that config 0 resolves to for these arguments in a dense call (the mask is
-// not an argument here; a causal call counts q-tile pairs, see above), -1 for
-// a NULL pointer.
+// not an argument here; a causal call counts q-tile pairs, see above, and
+// fav4_bshd_select_config_masked reports its choice), -1 for a NULL pointer.
 extern "C" int fav4_bshd_select_config(const Fav4Args* args);
+// No counterpart in the reference: the config ID config 0 resolves to for a
+// call with this mask (causal 0 or 1), for callers that label causal runs;
+// -1 for a NULL pointer or another mask value.
+extern "C" int fav4_bshd_select_config_masked(const Fav4Args* args, int causal);
 
 // ---- Split-KV forward --------------------------------------------------------
 // No counterpart in the reference.  It is for callers whose B * H * ceil(Sq/256)

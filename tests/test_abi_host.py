@@ -52,7 +52,7 @@ def test_exports_exactly_the_c_abi():
                       "fav4_bshd_forward_splitkv_varlen", "fav4_bshd_splitkv_varlen_workspace_size",
                       "fav4_bshd_splitkv_varlen_select", "fav4_bshd_forward_splitkv_paged",
                       "fav4_bshd_splitkv_paged_workspace_size", "fav4_bshd_splitkv_paged_select",
-                      "fav4_bshd_forward_splitkv_gqa_noalloc"}, public
+                      "fav4_bshd_forward_splitkv_gqa_noalloc", "fav4_bshd_select_config_masked"}, public
 
 
 def test_ctypes_layout_matches_reference(Args):
@@ -139,6 +139,7 @@ def test_rejects_bad_causal_or_config(lib, Args, causal, config):
 def test_rejects_null_args(lib):
     assert lib.fav4_bshd_forward(None, 0, 0, None) == HIP_ERROR_INVALID_VALUE
     assert lib.fav4_bshd_select_config(None) == -1
+    assert lib.fav4_bshd_select_config_masked(None, 0) == -1
 
 
 @pytest.mark.parametrize("b,h,sq,want", [
@@ -153,6 +154,30 @@ def test_select_config(lib, Args, b, h, sq, want):
     fields.update(batch=b, heads=h, sq=sq)
     got = lib.fav4_bshd_select_config(C.byref(Args(**fields)))
     assert got == want and 1 <= got <= 3
+    assert lib.fav4_bshd_select_config_masked(C.byref(Args(**fields)), 0) == got
+
+
+@pytest.mark.parametrize("b,h,sq,want", [
+    (32, 8, 1024, 1), (32, 8, 4096, 2), (1, 32, 4096, 2), (1, 64, 4096, 2), (2, 16, 4096, 2),
+    (1, 16, 4096, 1), (1, 8, 8192, 1), (1, 8, 16384, 2), (1, 1, 32768, 1)])
+def test_select_config_masked_causal(lib, Args, b, h, sq, want):
+    """Closed form of Auto for a causal call on 256 CUs: config 1 for
+    Sq <= 1024 or fewer than 256 q-tile pairs (B*H*ceil(ceil(Sq/256)/2)),
+    else config 2.  The masks disagree at B1 H16 S4096 and B1 H8 S8192: 256
+    q tiles (dense: config 2) but 128 pairs (causal: config 1)."""
+    fields = _good(Args)
+    fields.update(batch=b, heads=h, sq=sq)
+    tiles = (sq + 255) // 256
+    pairs = b * h * ((tiles + 1) // 2)
+    assert want == (1 if sq <= 1024 or pairs < 256 else 2)
+    assert lib.fav4_bshd_select_config_masked(C.byref(Args(**fields)), 1) == want
+    if (b, h, sq) in ((1, 16, 4096), (1, 8, 8192)):
+        assert lib.fav4_bshd_select_config(C.byref(Args(**fields))) == 2
+
+
+@pytest.mark.parametrize("causal", [-1, 2, 3])
+def test_select_config_masked_rejects_other_masks(lib, Args, causal):
+    assert lib.fav4_bshd_select_config_masked(C.byref(Args(**_good(Args))), causal) == -1
 
 
 def test_runner_rejects_host_tensors():
