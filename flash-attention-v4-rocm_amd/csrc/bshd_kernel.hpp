@@ -1082,6 +1082,8 @@ __device__ __forceinline__ float sum32(float x) {
 template <int PER, bool VARLEN = false>
 __global__ __launch_bounds__(256) void combine_kernel(Fav4Args a, SplitArgs sp) {
     constexpr int RPB = 8 / PER, NT = PER * 32, MAXV = (MAX_SPLITS + NT - 1) / NT;
+    // Chunks per lane group: PER = 1, 2, 4 serve up to 8, 16, 32 chunks; 8 up to MAX_SPLITS.
+    constexpr int NS = PER == 8 ? (MAX_SPLITS + 7) / 8 : 8;
     __shared__ float wsh[RPB][MAX_SPLITS];   // chunk weights 2^(lse_b,s - max)
     __shared__ float2 red_m[8], red_s[8];    // per-group maxima, then sums
     __shared__ f32x4 part_acc[8][32];
@@ -1108,6 +1110,17 @@ __global__ __launch_bounds__(256) void combine_kernel(Fav4Args a, SplitArgs sp) 
                 live = qi < qe - qs;
                 qtok = int64_t(qs) + qi;
             }
+        }
+        // The partial O rows do not depend on the weights: their loads go out
+        // first, so that their latency overlaps the log-sum phase (one memory
+        // round per row block instead of three).  Lane group `part` holds
+        // chunks part, part + PER, ... (at most NS of them).
+        const float* op = sp.o_part + r * D + q4 * 4;
+        f32x4 xo[NS];
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            const int s = part + i * PER;
+            xo[i] = live && s < sp.splits ? *reinterpret_cast<const f32x4*>(op + s * slab * D) : f32x4{};
         }
         float vb[MAXV], vl[MAXV];
         float mb = -__builtin_inff(), ml = -__builtin_inff();
@@ -1162,12 +1175,13 @@ __global__ __launch_bounds__(256) void combine_kernel(Fav4Args a, SplitArgs sp) 
         // the weight keeps them out of the sum exactly.
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         if (live) {
-            const float* op = sp.o_part + r * D + q4 * 4;
-#pragma unroll 4
-            for (int s = part; s < sp.splits; s += PER) {
-                const f32x4 x = *reinterpret_cast<const f32x4*>(op + s * slab * D);
-                const float w = wsh[slot][s];
-                if (w > 0.f) acc += w * x;
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                const int s = part + i * PER;
+                if (s < sp.splits) {
+                    const float w = wsh[slot][s];
+                    if (w > 0.f) acc += w * xo[i];
+                }
             }
         }
         if constexpr (PER > 1) {
