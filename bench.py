@@ -617,7 +617,9 @@ def loaded_telemetry(torch, fn, stream, launches=50, max_s=20.0):
             for _ in range(launches):
                 fn()
     got = {}
-    reader = threading.Thread(target=lambda: (time.sleep(0.3), got.update(t=gpu_telemetry())))
+    # amd-smi's activity figure averages over about a second: start it a
+    # second into the replays so the window holds load only.
+    reader = threading.Thread(target=lambda: (time.sleep(1.0), got.update(t=gpu_telemetry())))
     t_end = time.perf_counter() + max_s
     with torch.cuda.stream(stream):
         g.replay()
