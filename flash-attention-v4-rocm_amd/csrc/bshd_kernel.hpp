@@ -196,12 +196,11 @@ __device__ __forceinline__ void tile_mask(f32x16 (&s)[BN / 32], int start, int s
         const int lim = CAUSAL ? min(sk - 1, row) : sk - 1;   // last visible key of this row
 #pragma unroll
         for (int kb = 0; kb < BN / 32; ++kb) {
-            const int kl = start + kb * 32 + half * 4;
+            // Score v holds key kl + (v / 4) * 8 + v % 4: compare that small
+            // constant with lim - kl, one subtraction per block.
+            const int d = lim - (start + kb * 32 + half * 4);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int key = kl + (v >> 2) * 8 + (v & 3);
-                s[kb][v] = key > lim ? -__builtin_inff() : s[kb][v];
-            }
+            for (int v = 0; v < 16; ++v) s[kb][v] = (v >> 2) * 8 + (v & 3) > d ? -__builtin_inff() : s[kb][v];
         }
     }
 }
@@ -566,10 +565,15 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
                     step(S0{}, Plain{}, t);
                     step(S1{}, Plain{}, t + 1);
                 }
-                for (; t < ntiles; ++t) {
-                    if (t & 1) step(S1{}, Masked{}, t);
-                    else step(S0{}, Masked{}, t);
+                // t is even here, so the masked tiles also run in compile-time
+                // stage pairs: a runtime choice between two step bodies made
+                // the register allocator give O two homes and copy it (64-128
+                // moves) on every masked step.
+                for (; t + 1 < ntiles; t += 2) {
+                    step(S0{}, Masked{}, t);
+                    step(S1{}, Masked{}, t + 1);
                 }
+                if (t < ntiles) step(S0{}, Masked{}, t);
             }
         } else {
             for (; t + 2 < nfull; t += 3) {
@@ -857,12 +861,15 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
                     step(S1{}, Plain{}, t + 1);
                     step(S2{}, Plain{}, t + 2);
                 }
-                for (; t < t1; ++t) {
-                    const int r = (t - t0) % 3;
-                    if (r == 0) step(S0{}, Masked{}, t);
-                    else if (r == 1) step(S1{}, Masked{}, t);
-                    else step(S2{}, Masked{}, t);
+                // (t - t0) % 3 == 0 here: the masked tiles run in compile-time
+                // stage triples as well, so O keeps one register home.
+                for (; t + 2 < t1; t += 3) {
+                    step(S0{}, Masked{}, t);
+                    step(S1{}, Masked{}, t + 1);
+                    step(S2{}, Masked{}, t + 2);
                 }
+                if (t < t1) step(S0{}, Masked{}, t);
+                if (t + 1 < t1) step(S1{}, Masked{}, t + 1);
             }
         }
 
@@ -1021,10 +1028,13 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
                     step(S0{}, Plain{}, t);
                     step(S1{}, Plain{}, t + 1);
                 }
-                for (; t < ntiles; ++t) {
-                    if (t & 1) step(S1{}, Masked{}, t);
-                    else step(S0{}, Masked{}, t);
+                // Masked tiles in compile-time stage pairs too (t is even):
+                // no runtime choice of step body, so O keeps one home.
+                for (; t + 1 < ntiles; t += 2) {
+                    step(S0{}, Masked{}, t);
+                    step(S1{}, Masked{}, t + 1);
                 }
+                if (t < ntiles) step(S0{}, Masked{}, t);
             }
         }
 
