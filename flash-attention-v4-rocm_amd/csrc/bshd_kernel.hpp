@@ -376,7 +376,7 @@ __device__ __forceinline__ void pv_plain(const unsigned char* vs, const LdsOffse
 template <int WAVES, int BN, bool CAUSAL, bool LSE, int STAGES, bool PIPE = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
-    static_assert(!PIPE || STAGES == 3, "the cross-tile pipeline keeps three tiles in LDS");
+    static_assert(PIPE ? STAGES == 3 : STAGES == 2, "two stages, or three with the cross-tile pipeline");
     constexpr int BM = WAVES * 32;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
     constexpr int STAGE_BYTES = 2 * TILE_BYTES;          // K then V
@@ -477,7 +477,6 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
         };
         using S0 = std::integral_constant<int, 0>;
         using S1 = std::integral_constant<int, 1>;
-        using S2 = std::integral_constant<int, 2>;
         using Plain = std::integral_constant<bool, false>;
         using Masked = std::integral_constant<bool, true>;
         int t = 0;
@@ -574,18 +573,6 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
                     step(S1{}, Masked{}, t + 1);
                 }
                 if (t < ntiles) step(S0{}, Masked{}, t);
-            }
-        } else {
-            for (; t + 2 < nfull; t += 3) {
-                step(S0{}, Plain{}, t);
-                step(S1{}, Plain{}, t + 1);
-                step(S2{}, Plain{}, t + 2);
-            }
-            for (; t < ntiles; ++t) {
-                const int r = t % 3;
-                if (r == 0) step(S0{}, Masked{}, t);
-                else if (r == 1) step(S1{}, Masked{}, t);
-                else step(S2{}, Masked{}, t);
             }
         }
 
