@@ -107,19 +107,25 @@ def bits(torch, t):
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def check_rows(torch, orc, q, k, v, o, causal, pairs):
-    """FP64 oracle on the reference's sampled rows for the given (b, h) pairs.
-    Only those slices are copied to the host (a full S32768 tensor is 2 GiB)."""
+def check_rows(torch, orc, q, k, v, o, causal, pairs, lse=None):
+    """FP64 oracle on the reference's sampled rows for the given (b, h) pairs
+    (and the LSE of those rows when `lse` is given).  Only those slices are
+    copied to the host (a full S32768 tensor is 2 GiB)."""
     s = q.shape[1]
     rows = orc.sample_rows(s)
     rows_t = torch.from_numpy(rows).to(q.device)
-    refs, gots = [], []
+    refs, gots, ref_l, got_l = [], [], [], []
     for b, h in pairs:
         sl = lambda t: bits(torch, t[b:b + 1, :, h:h + 1])
-        ref, _ = orc.attention_fp64(sl(q), sl(k), sl(v), orc.DEFAULT_SCALE, causal, rows=rows)
+        ref, rl = orc.attention_fp64(sl(q), sl(k), sl(v), orc.DEFAULT_SCALE, causal, rows=rows)
         refs.append(ref[0, :, 0])
         gots.append(bits(torch, o[b:b + 1].index_select(1, rows_t)[:, :, h:h + 1])[0, :, 0])
-    return orc.errors(np.stack(gots), None, np.stack(refs), None), rows
+        if lse is not None:
+            ref_l.append(rl[0, 0])
+            got_l.append(lse[b, h].index_select(0, rows_t).cpu().numpy())
+    if lse is None:
+        return orc.errors(np.stack(gots), None, np.stack(refs), None), rows
+    return orc.errors(np.stack(gots), np.stack(got_l), np.stack(refs), np.stack(ref_l)), rows
 
 
 def time_graph(torch, fn, steps, warmup, observations, stream, spin_ms=0.0):
@@ -684,7 +690,7 @@ def headline(torch, orc, runner, args, b, h, s, stream, pairs, spin_ms=0.0, obse
     out = {}
     for causal in ([False] if args.no_causal else [False, True]):
         fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
-        check = None
+        check = check_lse = None
         if not args.no_check:
             o.fill_(float("nan"))
             torch.cuda.synchronize()   # the fill runs on the default stream
@@ -694,15 +700,28 @@ def headline(torch, orc, runner, args, b, h, s, stream, pairs, spin_ms=0.0, obse
             check, _ = check_rows(torch, orc, q, k, v, o, causal, pairs)
             if not orc.check_acceptance_tolerance(check):
                 raise SystemExit(f"sampled-row check failed (B{b} H{h} S{s} causal={causal}): {check}")
+            # The same rows with the LSE written (benchmarks/bshd.py:147-156
+            # checks every timed shape with and without it).
+            lse = torch.full((b, h, s), float("nan"), device=q.device, dtype=torch.float32)
+            o.fill_(float("nan"))
+            torch.cuda.synchronize()
+            with torch.cuda.stream(stream):
+                runner.call(q, k, v, o, lse, causal, args.config, stream=stream.cuda_stream)
+            torch.cuda.synchronize()
+            check_lse, _ = check_rows(torch, orc, q, k, v, o, causal, pairs, lse=lse)
+            del lse
+            if not orc.check_acceptance_tolerance(check_lse):
+                raise SystemExit(f"sampled-row LSE check failed (B{b} H{h} S{s} causal={causal}): {check_lse}")
         samples, tel = timed_with_telemetry(
             lambda: time_graph(torch, fn, args.steps, args.warmup, observations or args.observations, stream,
                                spin_ms=spin_ms))
         flop = orc.flops(b, h, s, s, causal)
         us = statistics.mean(samples)
         out[causal] = dict(us=us, median_us=statistics.median(samples), samples_us=samples,
-                           tflops=flop / us / 1e6, flop=flop, check=check, telemetry=tel)
+                           tflops=flop / us / 1e6, flop=flop, check=check, check_lse=check_lse, telemetry=tel)
         print(f"# B{b} H{h} S{s} causal={causal}: {us:.1f} us/launch, {flop / us / 1e6:.1f} TFLOP/s "
-              f"({flop / us / 1e6 / PEAK_BF16_TFLOPS * 100:.1f}% of peak) check={check}",
+              f"({flop / us / 1e6 / PEAK_BF16_TFLOPS * 100:.1f}% of peak) check={check} "
+              f"lse_max_abs={None if check_lse is None else check_lse['lse_max_abs']}",
               file=sys.stderr, flush=True)
     return out, (q, k, v, o)
 
@@ -761,7 +780,7 @@ def main():
             sweep[f"S{n}_{'causal' if causal else 'dense'}"] = dict(
                 us=round(r["us"], 2), tflops=round(r["tflops"], 1),
                 frac_of_peak=round(r["tflops"] / PEAK_BF16_TFLOPS, 4), check=r["check"],
-                telemetry=r["telemetry"])
+                check_lse=r["check_lse"], telemetry=r["telemetry"])
 
     traffic, counters_sha, stale = read_traffic(prov["library_sha256"])
     compulsory = 2 * b * h * 128 * (2 * s + 2 * s)
@@ -800,8 +819,11 @@ def main():
         line["causal"] = dict(value=round(c["tflops"], 2), unit="TFLOP/s", us_per_launch=round(c["us"], 3),
                               median_us_per_launch=round(c["median_us"], 3),
                               frac_of_peak=round(c["tflops"] / PEAK_BF16_TFLOPS, 4),
-                              samples_us=[round(x, 2) for x in c["samples_us"]], telemetry=c["telemetry"])
+                              samples_us=[round(x, 2) for x in c["samples_us"]], check=c["check"],
+                              check_lse=c["check_lse"], telemetry=c["telemetry"])
     line["dense_samples_us"] = [round(x, 2) for x in dense["samples_us"]]
+    line["dense_check"] = dense["check"]
+    line["dense_check_lse"] = dense["check_lse"]
     line["dense_telemetry"] = dense["telemetry"]
     line["comparator"] = cmp
     line["splitkv"] = skv
