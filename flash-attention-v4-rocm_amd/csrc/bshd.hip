@@ -294,10 +294,20 @@ int launch_split(const Fav4Args& a, int kv_heads, const SplitPlan& p, void* ws, 
     return hipGetLastError();
 }
 
+// causal = 2 on the packed calls: bottom-right causal (query i of a sequence
+// with sq queries and sk keys sees keys j <= sk - sq + i).
+constexpr int BOTTOM_RIGHT = 2;
+
 template <int WAVES>
 void launch_varlen(const Fav4VarlenArgs& a, int causal, int tiles, int total, int grid, hipStream_t stream) {
     const dim3 block(WAVES * 64);
-    if (causal && a.lse)
+    if (causal == BOTTOM_RIGHT && a.lse)
+        hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, true, true, WAVES, true>), dim3(grid), block, 0, stream, a,
+                           tiles, total);
+    else if (causal == BOTTOM_RIGHT)
+        hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, true, false, WAVES, true>), dim3(grid), block, 0, stream, a,
+                           tiles, total);
+    else if (causal && a.lse)
         hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, true, true, WAVES>), dim3(grid), block, 0, stream, a, tiles, total);
     else if (causal)
         hipLaunchKernelGGL((fav4::fwd_kernel_varlen<64, true, false, WAVES>), dim3(grid), block, 0, stream, a, tiles, total);
@@ -308,11 +318,12 @@ void launch_varlen(const Fav4VarlenArgs& a, int causal, int tiles, int total, in
 }
 
 // Checks of the packed-sequence arguments (before any HIP call); the shape
-// checks alone serve the queries that take no buffers.
+// checks alone serve the queries that take no buffers.  causal 0, 1 or
+// BOTTOM_RIGHT.
 int varlen_shape_ok(const Fav4VarlenArgs* a, int causal) {
     if (!a || a->batch <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->heads % a->kv_heads != 0 ||
         a->max_seqlen_q <= 0 || a->max_seqlen_k <= 0 || a->total_q <= 0 || a->total_k <= 0 ||
-        (causal != 0 && causal != 1) || !std::isfinite(a->scale) || a->scale <= 0)
+        causal < 0 || causal > BOTTOM_RIGHT || !std::isfinite(a->scale) || a->scale <= 0)
         return hipErrorInvalidValue;
     if (a->batch > INT_MAX - 1 || a->heads > INT_MAX / 256 ||
         int64_t(a->max_seqlen_q) * a->heads * 256 > int64_t(UINT32_MAX) ||
@@ -372,11 +383,10 @@ SplitPlan packed_split_plan(const Fav4Args& a, int kv_heads, int64_t total_k, in
     return p;
 }
 
-// causal = 2 in the packed decode calls: bottom-right causal (query i of a
-// sequence with sq queries and sk keys sees keys j <= sk - sq + i).  It sees
-// as many keys as a dense call, so it is planned like one, and it always runs
-// the split kernels (the unsplit packed forward has no such mask).
-constexpr int BOTTOM_RIGHT = 2;
+// Bottom-right causal in the split-KV packed calls sees as many keys as a
+// dense call, so it is planned like one, and it always runs the split
+// kernels, also for one chunk (the unsplit packed forward takes this mask
+// directly, with no workspace).
 
 SplitPlan varlen_split_plan(const Fav4VarlenArgs& v, int causal, int req) {
     const Fav4Args a = varlen_shape(v);

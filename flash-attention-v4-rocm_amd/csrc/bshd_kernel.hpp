@@ -895,10 +895,14 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
 // q tile up to max_seqlen_q); items past a sequence's end do nothing.  The
 // offsets read from device memory are clamped to [0, total] and to the
 // maximum lengths, so every access stays inside the caller's buffers.
+// BR (with CAUSAL): bottom-right causal, query i of a sequence with sq queries
+// and sk keys sees keys j <= sk - sq + i; with sq > sk the first sq - sk rows
+// see none and give O = 0, LSE = -inf.
 // ---------------------------------------------------------------------------
-template <int BN, bool CAUSAL, bool LSE, int WAVES>
+template <int BN, bool CAUSAL, bool LSE, int WAVES, bool BR = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
+    static_assert(!BR || CAUSAL, "bottom-right is a causal mask");
     constexpr int BM = WAVES * 32;
     constexpr int TILE_BYTES = BN * ROW_BYTES;
     constexpr int STAGE_BYTES = 2 * TILE_BYTES;
@@ -958,9 +962,14 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
                                     uint32_t(sq - q0 - 1) * row_bytes + ROW_BYTES);
         const rsrc_t ro = make_rsrc(static_cast<char*>(a.o) + qrow0 * ROW_BYTES,
                                     uint32_t(sq - q0 - 1) * row_bytes + ROW_BYTES);
-        const int kend = CAUSAL ? min(sk, q0 + BM) : sk;
+        // Key tiles [0, nfull) are unmasked for every row of the q tile;
+        // BR: up to the last row's diagonal, and unmasked below the first
+        // row's (shift = sk - sq; may be negative).
+        const int shift = BR ? sk - sq : 0;
+        const int kend = !CAUSAL ? sk : BR ? min(sk, max(0, min(sq, q0 + BM) + shift)) : min(sk, q0 + BM);
         const int ntiles = (kend + BN - 1) / BN;
-        const int nfull = (CAUSAL ? min(sk, q0 + 1) : sk) / BN;
+        const int nfull = (!CAUSAL ? sk : BR ? max(0, min(sk, q0 + 1 + shift)) : min(sk, q0 + 1)) / BN;
+        const int climit = row + shift;    // last visible key of this lane's row (causal)
 
         RowState st;
 #pragma unroll
@@ -993,9 +1002,10 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
                 __syncthreads();
                 if (t + 1 < ntiles) issue(t + 1);
                 // A causal tile entirely above this wave's rows changes nothing.
-                if (!(decltype(masked_c)::value && CAUSAL) || t * BN <= qw + 31)
-                    attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE>(cur, cur + TILE_BYTES, off, qr, st,
-                                                                           t == 0, t * BN, sk, row, half, scale2);
+                // BR rows that see no key yet keep a -inf base (EMPTY).
+                if (!(decltype(masked_c)::value && CAUSAL) || t * BN <= qw + 31 + shift)
+                    attend_fused<BN, decltype(masked_c)::value, CAUSAL, LSE, BR>(
+                        cur, cur + TILE_BYTES, off, qr, st, t == 0, t * BN, sk, climit, half, scale2);
             };
             using S0 = std::integral_constant<int, 0>;
             using S1 = std::integral_constant<int, 1>;

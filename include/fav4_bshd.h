@@ -131,7 +131,11 @@ extern "C" int fav4_bshd_forward_gqa(const Fav4Args* args, int kv_heads, int cau
 // sequence is attended on its own (top-left causal within the sequence when
 // causal = 1), exactly as fav4_bshd_forward would on that sequence alone
 // (bitwise, for sequences of at least one key).  A sequence with no keys gets
-// O = 0 and LSE = -inf.  GQA as in fav4_bshd_forward_gqa.
+// O = 0 and LSE = -inf.  GQA as in fav4_bshd_forward_gqa.  causal = 2:
+// bottom-right causal, query i of a sequence with sq queries and sk keys sees
+// keys j <= sk - sq + i (a prefill chunk against a cache); with sq > sk the
+// first sq - sk rows see none and get O = 0, LSE = -inf.  For sq = sk it is
+// bitwise the causal = 1 result.
 struct Fav4VarlenArgs {
     const void *q, *k, *v;             // BF16 [total_q | total_k, heads | kv_heads, 128], contiguous
     void *o;                           // BF16 [total_q, heads, 128], contiguous
@@ -171,7 +175,8 @@ extern "C" int fav4_bshd_forward_varlen(const Fav4VarlenArgs* args, int causal, 
 // prefill plan at the max lengths, counting for each 256-row q tile only the
 // keys up to its last row's diagonal (chunks past it are empty and end at
 // once).  It always runs the split kernels, one chunk included (with a
-// workspace).  Same argument contract
+// workspace); fav4_bshd_forward_varlen takes the same mask with none.  Same
+// argument contract
 // as fav4_bshd_forward_varlen (O and LSE rows, empty sequences, offset
 // clamping), plus:
 //  * splits: 0 = library choice (the chunk size the contiguous split-KV Auto

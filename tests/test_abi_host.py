@@ -409,7 +409,7 @@ def test_varlen_rejects_bad_arguments(lib, name, change):
     assert lib.fav4_bshd_forward_varlen(C.byref(a), 0, None) == HIP_ERROR_INVALID_VALUE
 
 
-@pytest.mark.parametrize("causal", [-1, 2])
+@pytest.mark.parametrize("causal", [-1, 3])
 def test_varlen_rejects_bad_causal(lib, causal):
     a = load_package().VarlenArgs(**_vgood())
     assert lib.fav4_bshd_forward_varlen(C.byref(a), causal, None) == HIP_ERROR_INVALID_VALUE

@@ -10,7 +10,9 @@ key rows [cu_k[b], cu_k[b+1]) of the packed K/V.  Pins:
     (wrong sequence, head or row);
   * the FP64 oracle on every sequence, at the reference harness's bar;
   * a sequence without keys gives O = 0 and LSE = -inf, one without queries
-    writes nothing, and rows outside O / LSE are never written.
+    writes nothing, and rows outside O / LSE are never written;
+  * bottom-right causal (causal = 2) against the FP64 bottom-right reference,
+    and bitwise the top-left call on sequences with as many queries as keys.
 """
 import numpy as np
 import pytest
@@ -153,3 +155,43 @@ def test_varlen_loose_max_seqlen_and_long_sequences(gpu_runner):
             o_ref, l_ref = _alone(gpu_runner, q[a:b], k[c:d], v[c:d], h, kvh, causal)
             assert torch.equal(o[a:b].view(torch.int16), o_ref.view(torch.int16)), (i, causal)
             assert torch.equal(lse[:, a:b].view(torch.int32), l_ref.view(torch.int32)), (i, causal)
+
+
+# (heads, kv_heads, [(sq, sk), ...]) for bottom-right causal: sq < sk (a
+# prefill chunk against a cache), sq = sk, sq > sk (the first sq - sk rows see
+# no key), sequences without keys or queries, several q tiles.  The first batch
+# runs 128-row workgroups (max_seqlen_q <= 1024), the second 256-row ones
+# (6 x 8 x 6 (sequence, head, q tile) items, more than the 256 CUs).
+BR_CASES = [
+    (8, 2, [(300, 3000), (129, 129), (700, 100), (64, 1), (0, 40), (5, 0), (1, 2049), (513, 1000)]),
+    (8, 8, [(1500, 4000), (1100, 1100), (1300, 600), (2, 9), (1024, 1500), (257, 300)]),
+]
+
+
+@pytest.mark.parametrize("case", BR_CASES, ids=["bm128", "bm256"])
+def test_varlen_bottom_right_causal(gpu_runner, case):
+    """causal = 2: every sequence against the FP64 bottom-right reference (rows
+    that see no key: O = 0, LSE = -inf exactly), nothing written past O / LSE,
+    O without LSE bitwise O with it, and sequences with sq = sk bitwise the
+    top-left (causal = 1) call."""
+    import torch
+    from tests.test_gpu_splitkv_paged import _check_bottom_right
+    h, kvh, lens = case
+    q, k, v, cu_q, cu_k = _pack(h, kvh, lens, seed=71)
+    dev = torch.device("cuda:0")
+    qd, kd, vd = to_device(q, dev), to_device(k, dev), to_device(v, dev)
+    max_q, max_k = max(s for s, _ in lens), max(s for _, s in lens)
+    print(f"  varlen bottom-right h{h} kv{kvh} max_q {max_q} max_k {max_k}", flush=True)
+    o, lse, og, lg = _run_varlen(gpu_runner, qd, kd, vd, cu_q, cu_k, max_q, max_k, 2, True)
+    assert torch.isnan(og).all().item() and torch.isnan(lg).all().item()
+    assert not torch.isnan(o.float()).any().item() and not torch.isnan(lse).any().item()
+    _check_bottom_right(o, lse, q, k, v, cu_q, cu_k, lens, h // kvh, "unsplit")
+    o_nl, _, og_nl, _ = _run_varlen(gpu_runner, qd, kd, vd, cu_q, cu_k, max_q, max_k, 2, False)
+    assert torch.equal(o.view(torch.int16), o_nl.view(torch.int16))
+    assert torch.isnan(og_nl).all().item()
+    o_tl, lse_tl, _, _ = _run_varlen(gpu_runner, qd, kd, vd, cu_q, cu_k, max_q, max_k, 1, True)
+    for i, (sq, sk) in enumerate(lens):
+        a, b = cu_q[i], cu_q[i + 1]
+        if sq == sk and sq > 0:
+            assert torch.equal(o[a:b].view(torch.int16), o_tl[a:b].view(torch.int16)), i
+            assert torch.equal(lse[:, a:b].view(torch.int32), lse_tl[:, a:b].view(torch.int32)), i
