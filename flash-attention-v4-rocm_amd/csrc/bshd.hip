@@ -384,9 +384,10 @@ SplitPlan packed_split_plan(const Fav4Args& a, int kv_heads, int64_t total_k, in
 }
 
 // Bottom-right causal in the split-KV packed calls sees as many keys as a
-// dense call, so it is planned like one, and it always runs the split
-// kernels, also for one chunk (the unsplit packed forward takes this mask
-// directly, with no workspace).
+// dense call, so it is planned like one.  Decode always runs the split
+// kernels, also for one chunk (their one-wave shape streams a K/V head once
+// for its whole query group); prefill with one chunk runs the unsplit packed
+// forward, which takes this mask directly.
 
 SplitPlan varlen_split_plan(const Fav4VarlenArgs& v, int causal, int req) {
     const Fav4Args a = varlen_shape(v);
@@ -405,9 +406,9 @@ int varlen_split_ok(const Fav4VarlenArgs* v, int causal, int splits, bool buffer
     return split_shape_ok(&a, v->kv_heads, br ? 0 : causal, splits);
 }
 
-// Workspace of a packed plan; bottom-right causal needs it for one chunk too.
+// Workspace of a packed plan; bottom-right decode needs it for one chunk too.
 int64_t varlen_workspace(const Fav4VarlenArgs& v, const SplitPlan& p, int causal) {
-    if (p.splits <= 1 && causal != BOTTOM_RIGHT) return 0;
+    if (p.splits <= 1 && (causal != BOTTOM_RIGHT || v.max_seqlen_q > DECODE_SQ)) return 0;
     return int64_t(p.splits) * v.batch * v.heads * v.max_seqlen_q * (fav4::D * 4 + 2 * 4);
 }
 
@@ -648,9 +649,11 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_splitkv_
     if (st != hipSuccess) return st;
     const SplitPlan p = varlen_split_plan(*a, causal, splits);
     // Top-left causal decode (max_seqlen_q <= 32) sees at most 32 keys, one
-    // tile: the plan never splits it.
+    // tile: the plan never splits it.  One-chunk bottom-right prefill needs
+    // no merge either.
     const bool br = causal == BOTTOM_RIGHT;
-    if (!br && (p.splits == 1 || causal)) return fav4_bshd_forward_varlen(a, causal, stream);
+    const bool unsplit = br ? p.splits == 1 && a->max_seqlen_q > DECODE_SQ : p.splits == 1 || causal;
+    if (unsplit) return fav4_bshd_forward_varlen(a, causal, stream);
     const Fav4Args shape = varlen_shape(*a);
     const int64_t need = varlen_workspace(*a, p, causal);
     if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255) || uint64_t(need) > workspace_bytes)

@@ -174,9 +174,9 @@ extern "C" int fav4_bshd_forward_varlen(const Fav4VarlenArgs* args, int causal, 
 // dense call; prefill (max_seqlen_q > 32, 8-wave kernels) with the contiguous
 // prefill plan at the max lengths, counting for each 256-row q tile only the
 // keys up to its last row's diagonal (chunks past it are empty and end at
-// once).  It always runs the split kernels, one chunk included (with a
-// workspace); fav4_bshd_forward_varlen takes the same mask with none.  Same
-// argument contract
+// once).  Decode always runs the split kernels, one chunk included (with a
+// workspace); prefill with one chunk runs fav4_bshd_forward_varlen, which
+// takes the same mask, and needs none.  Same argument contract
 // as fav4_bshd_forward_varlen (O and LSE rows, empty sequences, offset
 // clamping), plus:
 //  * splits: 0 = library choice (the chunk size the contiguous split-KV Auto

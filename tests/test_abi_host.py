@@ -495,9 +495,10 @@ def test_splitkv_varlen_rejects_bad_arguments(lib, name, change):
 
 
 def test_splitkv_varlen_bottom_right(lib):
-    """causal = 2 (bottom-right) is planned like a dense call and always
+    """causal = 2 (bottom-right) is planned like a dense call; decode always
     splits (one chunk needs a workspace too); longer queries take the dense
-    prefill plan."""
+    prefill plan, and with one chunk the unsplit packed forward (no
+    workspace)."""
     f = _vgood()
     f.update(q=None, k=None, v=None, o=None, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=4, max_seqlen_k=5000)
     a = load_package().VarlenArgs(**f)
@@ -513,6 +514,7 @@ def test_splitkv_varlen_bottom_right(lib):
     n, _ = _split_plan(3, 4, 600, 5000, 0, cus=256, kvh=2)
     assert lib.fav4_bshd_splitkv_varlen_select(C.byref(a), 2) == n
     assert lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), 2, 0) == n * 3 * 4 * 600 * 520
+    assert lib.fav4_bshd_splitkv_varlen_workspace_size(C.byref(a), 2, 1) == 0
     assert lib.fav4_bshd_splitkv_varlen_select(C.byref(a), 0) == 1
     p = _pgood(q=None, k_cache=None, v_cache=None, o=None, cu_seqlens_q=None, seqlens_k=None, block_table=None)
     assert lib.fav4_bshd_splitkv_paged_select(C.byref(p), 2) == lib.fav4_bshd_splitkv_paged_select(C.byref(p), 0) > 0

@@ -172,8 +172,9 @@ BR_CASES = [
 def test_varlen_bottom_right_causal(gpu_runner, case):
     """causal = 2: every sequence against the FP64 bottom-right reference (rows
     that see no key: O = 0, LSE = -inf exactly), nothing written past O / LSE,
-    O without LSE bitwise O with it, and sequences with sq = sk bitwise the
-    top-left (causal = 1) call."""
+    O without LSE bitwise O with it, the one-chunk split-KV packed call
+    bitwise this one, and sequences with sq = sk bitwise the top-left
+    (causal = 1) call."""
     import torch
     from tests.test_gpu_splitkv_paged import _check_bottom_right
     h, kvh, lens = case
@@ -189,6 +190,15 @@ def test_varlen_bottom_right_causal(gpu_runner, case):
     o_nl, _, og_nl, _ = _run_varlen(gpu_runner, qd, kd, vd, cu_q, cu_k, max_q, max_k, 2, False)
     assert torch.equal(o.view(torch.int16), o_nl.view(torch.int16))
     assert torch.isnan(og_nl).all().item()
+    # the split-KV packed call with one chunk takes this kernel (no workspace)
+    assert gpu_runner.splitkv_varlen_workspace_size(len(lens), h, kvh, max_q, max_k, len(q), len(k), 2, 1) == 0
+    o_s = torch.full_like(o, float("nan"))
+    lse_s = torch.full_like(lse, float("nan"))
+    gpu_runner.call_splitkv_varlen(qd, kd, vd, o_s, lse_s, torch.from_numpy(cu_q).to(dev),
+                                   torch.from_numpy(cu_k).to(dev), max_q, max_k, 2, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), o_s.view(torch.int16))
+    assert torch.equal(lse.view(torch.int32), lse_s.view(torch.int32))
     o_tl, lse_tl, _, _ = _run_varlen(gpu_runner, qd, kd, vd, cu_q, cu_k, max_q, max_k, 1, True)
     for i, (sq, sk) in enumerate(lens):
         a, b = cu_q[i], cu_q[i + 1]
