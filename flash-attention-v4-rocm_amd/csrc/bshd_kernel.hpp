@@ -719,19 +719,39 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
 
     // Rows of one item's row space: a head's queries, or a group's.
     const int rows = PACK ? group * a.sq : a.sq;
+    const int items_per_batch = PACK ? kv_heads : a.heads;
+    const int npairs = a.batch * items_per_batch, full = npairs >> 3, rem8 = npairs & 7;
     for (int id = blockIdx.x; id < total; id += gridDim.x) {
         // XCD-contiguous order; within a (b, h) -- PACK: (b, K/V head) -- the
         // q tiles of one key chunk are adjacent, so they share it in L2.
         const int xcd = id & 7, slot = id >> 3, per = total >> 3, rem = total & 7;
         const int logical = xcd * per + min(xcd, rem) + slot;
         const int per_item = tiles * sp.splits;
-        const int it = __builtin_amdgcn_readfirstlane(logical / per_item);
+        int it = __builtin_amdgcn_readfirstlane(logical / per_item);
         const int r = __builtin_amdgcn_readfirstlane(logical - it * per_item);
+        if constexpr (VARLEN) {
+            // Packed sequences differ in length: take the (sequence, head)
+            // pairs column by column from an 8-wide grid (it = 8 * row + col,
+            // as fwd_kernel_varlen does), so XCD x works on the pairs with
+            // it % 8 == x -- a share of every sequence -- instead of a few
+            // whole sequences.  With 8 K/V heads each XCD gets one head of
+            // every sequence.
+            const int j = it;
+            int gcol, grow;
+            if (j < rem8 * (full + 1)) {
+                gcol = j / (full + 1);
+                grow = j - gcol * (full + 1);
+            } else {
+                const int jj = j - rem8 * (full + 1);
+                gcol = rem8 + jj / full;
+                grow = jj - (gcol - rem8) * full;
+            }
+            it = __builtin_amdgcn_readfirstlane(grow * 8 + gcol);
+        }
         const int split = r / tiles, tile = r - split * tiles;
 
         // it = b*heads + h, or (PACK) b*kv_heads + K/V head; head0 = the first
         // query head of the item's rows.
-        const int items_per_batch = PACK ? kv_heads : a.heads;
         const int batch = it / items_per_batch, unit = it - batch * items_per_batch;
         const int head0 = PACK ? unit * group : unit;
         const int bh = batch * a.heads + head0;
