@@ -141,21 +141,22 @@ __device__ __forceinline__ DmaOffsets<DMA> dma_offsets(int wave, int lane, uint3
 // DMA of one K and one V tile (descriptors rk / rv start at the tile's first
 // row) to the LDS byte addresses k_lds and v_lds: this wave's DMA ops land at
 // 1 KiB slots wave * DMA + i of each tile.
-template <int DMA>
+// NT: nontemporal loads, for K/V that no other workgroup reads again.
+template <int DMA, bool NT = false>
 __device__ __forceinline__ void dma_kv(u32x4 rk, u32x4 rv, uint32_t k_lds, uint32_t v_lds, int wave,
                                        const DmaOffsets<DMA>& d) {
     const uint32_t slot = wave * DMA * 1024;
 #pragma unroll
     for (int i = 0; i < DMA; ++i) {
-        dma16(rk, k_lds + slot + i * 1024, d.k[i]);
-        dma16(rv, v_lds + slot + i * 1024, d.v[i]);
+        dma16<NT>(rk, k_lds + slot + i * 1024, d.k[i]);
+        dma16<NT>(rv, v_lds + slot + i * 1024, d.v[i]);
     }
 }
 
 // The same into one LDS stage at byte address `stage`: K at +0, V at +TILE_BYTES.
-template <int DMA, int TILE_BYTES>
+template <int DMA, int TILE_BYTES, bool NT = false>
 __device__ __forceinline__ void dma_tile(u32x4 rk, u32x4 rv, uint32_t stage, int wave, const DmaOffsets<DMA>& d) {
-    dma_kv<DMA>(rk, rv, stage, stage + TILE_BYTES, wave, d);
+    dma_kv<DMA, NT>(rk, rv, stage, stage + TILE_BYTES, wave, d);
 }
 
 // S^T = K.Q^T for one tile: 8 MFMAs per 32-key block, K operands read ahead.
@@ -825,7 +826,7 @@ void fwd_kernel_split(Fav4Args a, SplitArgs sp, int kv_heads, int tiles, int tot
                 const uint32_t bytes = uint32_t(rows_left - 1) * kv_row_bytes + ROW_BYTES;
                 const u32x4 rk = make_desc(kbase + row0 * kv_row_bytes, bytes);
                 const u32x4 rv = make_desc(vbase + row0 * kv_row_bytes, bytes);
-                dma_tile<DMA, TILE_BYTES>(rk, rv, smem_base + ((t - t0) % STAGES) * STAGE_BYTES, wave, dofs);
+                dma_tile<DMA, TILE_BYTES, PACK>(rk, rv, smem_base + ((t - t0) % STAGES) * STAGE_BYTES, wave, dofs);
             };
             issue(t0);
             issue(t0 + 1);

@@ -67,15 +67,28 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // wait for the next tile's loads before reading the current tile).  Callers
 // retire these loads themselves with s_waitcnt vmcnt before a barrier.  M0 is
 // a reserved register for the compiler, so its value is saved and restored.
+// NT sets the load's nontemporal cache policy: for data read once (a decode's
+// K/V stream), measured to lift MI355X's read rate over many concurrent
+// 256-byte row streams from about 6.2 to 7.0 TB/s.
+template <bool NT = false>
 __device__ __forceinline__ void dma16(u32x4 desc, uint32_t lds, uint32_t voffset) {
     uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved) : "s"(lds), "v"(voffset), "s"(desc) : "memory");
+    if constexpr (NT)
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved) : "s"(lds), "v"(voffset), "s"(desc) : "memory");
+    else
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved) : "s"(lds), "v"(voffset), "s"(desc) : "memory");
 }
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

@@ -36,13 +36,14 @@ __global__ __launch_bounds__(WAVES * 64) void loader_probe(KatArgs a) {
 
     // The kernels' tile DMA: the slice's rows are row_bytes apart, the
     // descriptor starts at the tile's first row and ends at the slice's last.
+    // The one-wave shape loads nontemporally, as the split-KV decode does.
     const DmaOffsets<DMA> dofs = dma_offsets<DMA>(wave, lane, row_bytes, row_bytes);
     const int64_t slice = (int64_t(a.b) * a.sk * a.heads + a.h) * ROW_BYTES;
     const int first = a.t * BN;
     const uint32_t bound = uint32_t(a.sk - first - 1) * row_bytes + ROW_BYTES;
     const u32x4 rk = make_desc(a.k + slice + int64_t(first) * row_bytes, bound);
     const u32x4 rv = make_desc(a.v + slice + int64_t(first) * row_bytes, bound);
-    dma_tile<DMA, TILE_BYTES>(rk, rv, lds_addr(smem), wave, dofs);
+    dma_tile<DMA, TILE_BYTES, WAVES == 1>(rk, rv, lds_addr(smem), wave, dofs);
     wait_vmem();
     __syncthreads();
 
