@@ -1,0 +1,122 @@
+"""Size-independent properties of the forward at the headline size (B32 H8
+Sq=Sk=4096 D128), checked on every output element without the oracle.
+
+* Constant values. When every V row of a (batch, head) slice is the same
+  BF16 vector c, every output row is c bitwise. This holds dense and causal,
+  on every config. The weights, the O rescale and the final division by the
+  weight sum cancel exactly within BF16 rounding.
+* Causal prefix. With top-left causal masking, row i depends only on keys
+  j <= i. Rewriting the K/V rows from key m on leaves every row < m
+  bitwise unchanged, O and LSE, where m lies inside a q tile and a key
+  tile. This also holds when a wave's other rows move their softmax base:
+  a row whose base did not move is rescaled by exactly 1.
+* Slice independence. Rewriting one (batch, head) slice's Q, K and V
+  leaves every other slice bitwise unchanged.
+* Key and query tails. The strided entry point runs on views whose
+  sequence stride leaves spare rows between batches, and those rows hold
+  NaN. Sq = Sk = 4000 is not a multiple of any tile. O and LSE must be
+  bitwise the contiguous call's and finite. A NaN reaching a masked PV
+  product would show, since 0 * NaN = NaN. The O rows past sq keep their
+  sentinel.
+"""
+import pytest
+
+pytestmark = pytest.mark.gpu
+B, H, S = 32, 8, 4096
+
+
+def _inputs(torch, b, h, sq, sk, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    mk = lambda s: torch.randn((b, s, h, 128), device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
+    return mk(sq), mk(sk), mk(sk)
+
+
+def _run(torch, runner, q, k, v, causal, config):
+    o = torch.full_like(q, float("nan"))
+    lse = torch.full((q.shape[0], q.shape[2], q.shape[1]), float("nan"), device="cuda", dtype=torch.float32)
+    runner.call(q, k, v, o, lse, causal, config)
+    torch.cuda.synchronize()
+    return o, lse
+
+
+def _same(torch, x, y):
+    bits = torch.int16 if x.dtype == torch.bfloat16 else torch.int32
+    return torch.equal(x.contiguous().view(bits), y.contiguous().view(bits))
+
+
+@pytest.mark.parametrize("config", [0, 1, 2, 3])
+@pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
+def test_constant_values_give_that_value(gpu_runner, causal, config):
+    import torch
+    q, k, _ = _inputs(torch, B, H, S, S, seed=101)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(102)
+    c = torch.randn((B, 1, H, 128), device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
+    v = c.expand(B, S, H, 128).contiguous()
+    print(f"  constant V B{B} H{H} S{S} causal={causal} config={config}", flush=True)
+    o, lse = _run(torch, gpu_runner, q, k, v, causal, config)
+    assert _same(torch, o, c.expand_as(o)), "O differs from the constant V row"
+    assert torch.isfinite(lse).all().item()
+
+
+@pytest.mark.parametrize("config", [0, 1, 2, 3])
+def test_causal_prefix_ignores_later_keys(gpu_runner, config):
+    import torch
+    q, k, v = _inputs(torch, B, H, S, S, seed=201)
+    m = 2048 + 100
+    print(f"  causal prefix B{B} H{H} S{S} config={config} rewrite keys >= {m}", flush=True)
+    o1, l1 = _run(torch, gpu_runner, q, k, v, True, config)
+    k2, v2 = k.clone(), v.clone()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(202)
+    # Larger logits past m make the rows >= m of the shared waves move their base.
+    k2[:, m:] = (4 * torch.randn(k2[:, m:].shape, device="cuda", generator=g)).to(torch.bfloat16)
+    v2[:, m:] = torch.randn(v2[:, m:].shape, device="cuda", generator=g).to(torch.bfloat16)
+    o2, l2 = _run(torch, gpu_runner, q, k2, v2, True, config)
+    assert _same(torch, o1[:, :m], o2[:, :m]), "rows before the rewritten keys changed"
+    assert _same(torch, l1[:, :, :m], l2[:, :, :m]), "LSE of rows before the rewritten keys changed"
+    assert not _same(torch, o1[:, m:], o2[:, m:]), "rows after the rewritten keys did not change"
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
+def test_slices_are_independent(gpu_runner, causal):
+    import torch
+    q, k, v = _inputs(torch, B, H, S, S, seed=301)
+    bb, hh = 17, 5
+    print(f"  slice independence B{B} H{H} S{S} causal={causal} rewrite (b={bb}, h={hh})", flush=True)
+    o1, l1 = _run(torch, gpu_runner, q, k, v, causal, 0)
+    q2, k2, v2 = q.clone(), k.clone(), v.clone()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(302)
+    for x in (q2, k2, v2):
+        x[bb, :, hh] = torch.randn(x[bb, :, hh].shape, device="cuda", generator=g).to(torch.bfloat16)
+    o2, l2 = _run(torch, gpu_runner, q2, k2, v2, causal, 0)
+    keep = torch.ones((B, H), dtype=torch.bool, device="cuda")
+    keep[bb, hh] = False
+    assert _same(torch, o1.permute(0, 2, 1, 3)[keep], o2.permute(0, 2, 1, 3)[keep])
+    assert _same(torch, l1[keep], l2[keep])
+    assert not _same(torch, o1[bb, :, hh], o2[bb, :, hh])
+
+
+@pytest.mark.parametrize("config", [0, 1, 2, 3])
+@pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
+def test_nan_rows_past_the_tails_are_never_used(gpu_runner, causal, config):
+    import torch
+    s, pad = 4000, 96
+    q, k, v = _inputs(torch, B, H, s, s, seed=401)
+    print(f"  tails B{B} H{H} {s}x{s} in {s + pad}-row buffers causal={causal} config={config}", flush=True)
+    o_ref, l_ref = _run(torch, gpu_runner, q, k, v, causal, config)
+    bufs = []
+    for x in (q, k, v):
+        full = torch.full((B, s + pad, H, 128), float("nan"), device="cuda", dtype=torch.bfloat16)
+        full[:, :s] = x
+        bufs.append(full)
+    o_full = torch.full((B, s + pad, H, 128), 7.0, device="cuda", dtype=torch.bfloat16)
+    lse = torch.full((B, H, s), float("nan"), device="cuda", dtype=torch.float32)
+    gpu_runner.call_strided(bufs[0][:, :s], bufs[1][:, :s], bufs[2][:, :s], o_full[:, :s], lse, causal, config)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o_full[:, :s].float()).all().item(), "a NaN row past a tail reached the output"
+    assert _same(torch, o_full[:, :s], o_ref)
+    assert _same(torch, lse, l_ref)
+    assert (o_full[:, s:] == 7.0).all().item(), "rows past sq were written"
