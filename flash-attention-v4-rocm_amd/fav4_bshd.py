@@ -129,11 +129,22 @@ _LIB = None
 
 
 def load_library(path: Path = LIB_PATH) -> C.CDLL:
-    """Load the built library (raises OSError if it is missing)."""
+    """Load the built library (raises OSError if it is missing).
+
+    PyTorch-ROCm wheels bundle their own HIP and HSA runtimes. Torch is
+    therefore imported first when it is installed. The library's
+    libamdhip64.so.7 dependency then binds to the runtime already in the
+    process, and torch's streams and the library share one runtime.
+    Loaded the other way round, the process holds two HIP runtimes, and
+    the library's launches fail with hipErrorNoDevice (100)."""
     global _LIB
     if _LIB is None or Path(_LIB._name) != Path(path):
         if not Path(path).exists():
             raise OSError(f"{path} not built; run __graft_entry__.build() first")
+        try:
+            import torch  # noqa: F401  (binds the library to torch's HIP runtime)
+        except ImportError:
+            pass
         lib = C.CDLL(str(path))
         lib.fav4_bshd_forward.argtypes = [C.POINTER(Args), C.c_int, C.c_int, C.c_void_p]
         lib.fav4_bshd_forward.restype = C.c_int

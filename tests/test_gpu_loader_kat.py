@@ -33,6 +33,7 @@ HIP_ERROR_INVALID_VALUE = 1
 
 
 def _lib():
+    import torch  # noqa: F401  (torch's HIP runtime first, as the package's loader does)
     if not KAT_LIB.exists():
         import __graft_entry__
         __graft_entry__.import_package().build_library()
