@@ -68,6 +68,10 @@ def parse_args():
     p.add_argument("--no-api", action="store_true", help="skip the GQA / varlen report")
     p.add_argument("--no-telemetry", action="store_true",
                    help="start no child processes (amd-smi clocks, hipcc version), e.g. under a profiler")
+    p.add_argument("--mfma-ceiling", action="store_true",
+                   help="MFMA-only ceiling: a probe kernel streaming BF16 MFMAs (32x32x16 and 16x16x32) at the "
+                        "forward's occupancy, graph-timed with clock and power under load, beside the dense and "
+                        "causal headline in the same process; prints one JSON line")
     p.add_argument("--pmc-pass", action="store_true",
                    help="profiling mode for counter runs: two eager launches per mask type, then a "
                         "plain 1 GiB device copy (HBM counter calibration); prints no JSON")
@@ -91,6 +95,60 @@ def pmc_pass(torch, runner, args):
         dst.copy_(src)
     torch.cuda.synchronize()
     print("# pmc-pass copy: 1073741824 bytes read + 1073741824 bytes written per dispatch", flush=True)
+
+
+def mfma_ceiling(torch, runner, pkg, args):
+    """The MFMA rate with nothing else on the chip (libfav4_mfma_ceiling.so,
+    built by build()), at the clock the board's power limit allows, beside
+    the headline kernels measured the same way. One workgroup of 8 waves per
+    CU streams BF16 MFMAs on pseudo-random register operands; shape 0 is
+    32x32x16 (the forward's), shape 1 16x16x32 at equal FLOPs."""
+    import ctypes as C
+    lib = C.CDLL(str(pkg.CEILING_LIB_PATH))
+    lib.fav4_probe_mfma_ceiling.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    lib.fav4_probe_mfma_ceiling.restype = C.c_int
+    stream = torch.cuda.Stream()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 2048                                   # about 2 ms per launch
+    out = torch.empty(cus * 512, device="cuda", dtype=torch.float32)
+    res = {}
+    for shape, name in ((0, "mfma_32x32x16"), (1, "mfma_16x16x32")):
+        fn = lambda: lib.fav4_probe_mfma_ceiling(shape, cus, iters, out.data_ptr(), stream.cuda_stream)
+        with torch.cuda.stream(stream):
+            st = fn()
+        torch.cuda.synchronize()
+        if st:
+            raise SystemExit(f"mfma ceiling probe: HIP status {st}")
+        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+        flop = cus * 8 * iters * 1048576
+        res[name] = dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1),
+                         frac_of_peak=round(flop / us / 1e6 / PEAK_BF16_TFLOPS, 4),
+                         telemetry_under_load=loaded_telemetry(torch, fn, stream) if _TELEMETRY else None)
+        print(f"# {name}: {us:.1f} us, {flop / us / 1e6:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    b, h, s = args.batch, args.heads, args.seq
+    q, k, v = make_inputs(torch, b, h, s)
+    o = torch.empty_like(q)
+    for causal in (False, True):
+        fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
+        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+        tflops = flops(b, h, s, s, causal) / us / 1e6
+        res["fwd_causal" if causal else "fwd_dense"] = dict(
+            us=round(us, 2), tflops=round(tflops, 1), frac_of_peak=round(tflops / PEAK_BF16_TFLOPS, 4),
+            telemetry_under_load=loaded_telemetry(torch, fn, stream) if _TELEMETRY else None)
+        print(f"# B{b} H{h} S{s} causal={causal}: {us:.1f} us, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    res["fwd_dense_of_ceiling"] = round(res["fwd_dense"]["tflops"] / res["mfma_32x32x16"]["tflops"], 4)
+    print(json.dumps({"mode": "mfma_ceiling", "workload": f"B{b} H{h} Sq=Sk={s} D128 BF16, LSE off, config "
+                      f"{args.config}", "cus": cus, "iters_per_wave": iters, **res}), flush=True)
+
+
+def flops(b, h, sq, sk, causal):
+    """Useful QK+PV FLOPs, the reference's convention (benchmarks/bshd.py:169-170):
+    4*B*H*128*Sq*Sk dense; top-left causal counts the keys each row sees,
+    4*B*H*128*sum_{i<Sq} min(i+1, Sk)."""
+    if not causal:
+        return 4 * b * h * 128 * sq * sk
+    full = min(sq, sk)
+    return 4 * b * h * 128 * (full * (full + 1) // 2 + max(0, sq - sk) * sk)
 
 
 def make_inputs(torch, b, h, s, seed=11939):
@@ -235,7 +293,7 @@ def cpu_baseline(torch, orc, q, k, v, budget_s):
 
     done, elapsed = run(lambda p: orc.attention_fp64(qb, kb, vb, orc.DEFAULT_SCALE, False, heads=[p]), budget_s)
     done32, elapsed32 = run(lambda p: _attention_fp32_slice(qb, kb, vb, p, orc.DEFAULT_SCALE), budget_s / 2)
-    flop1 = orc.flops(1, 1, s, s, False)
+    flop1 = flops(1, 1, s, s, False)
     host = cpu_info()
     return dict(value=flop1 * done / elapsed / 1e12, unit="TFLOP/s", cores=cores, kind="port",
                 sample=f"FP64 numpy oracle, {done} of {len(pairs)} (b,h) slices of B{b} H{h} "
@@ -300,7 +358,7 @@ def comparator(torch, orc, runner, q, k, v, o, stream, args, causal_list):
             t[who].append(time_eager(torch, ours if who == "ours" else theirs, args.steps, args.warmup, stream))
         torch.cuda.synchronize()
         diff = (ref[0].transpose(1, 2).float() - o.float()).abs().max().item()
-        flop = orc.flops(b, h, s, s, causal)
+        flop = flops(b, h, s, s, causal)
         us_o, us_t = statistics.mean(t["ours"]), statistics.mean(t["theirs"])
         out["causal" if causal else "dense"] = dict(
             tflops=round(flop / us_t / 1e6, 2), us_per_launch=round(us_t, 3),
@@ -331,7 +389,7 @@ def splitkv_report(torch, orc, runner, args, stream):
                          dtype=torch.uint8)
         plain = lambda: runner.call(q, k, v, o, None, causal, 0, stream=stream.cuda_stream)
         split = lambda: runner.call_splitkv(q, k, v, o, None, causal, 0, workspace=ws, stream=stream.cuda_stream)
-        flop = orc.flops(b, h, sq, sk, causal)
+        flop = flops(b, h, sq, sk, causal)
         res = {"workload": f"B{b} H{h} Sq={sq} Sk={sk} D128 BF16 {'causal' if causal else 'dense'}, LSE off",
                "splits": splits, "workspace_bytes": ws.numel()}
         for name, fn in (("plain", plain), ("splitkv", split)):
@@ -389,7 +447,7 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
         checks = lambda: [(q[i:i + 1], k[i:i + 1].repeat_interleave(grp, dim=2),
                            v[i:i + 1].repeat_interleave(grp, dim=2), o[i:i + 1], causal) for i in (0, b - 1)]
         res["causal" if causal else "dense"] = measure(f"gqa causal={causal}", fn, o, checks,
-                                                       orc.flops(b, h, s, s, causal))
+                                                       flops(b, h, s, s, causal))
     out["gqa"] = res
     del q, k, v, o
 
@@ -405,7 +463,7 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
         fn = lambda: runner.call_varlen(q, k, v, o, None, cu, cu, maxlen, maxlen, causal, stream=stream.cuda_stream)
         sel = (0, int(np.argmax(lens)))
         checks = lambda: [tuple(x[cu_h[i]:cu_h[i + 1]][None] for x in (q, k, v, o)) + (causal,) for i in sel]
-        flop = sum(orc.flops(1, h, int(n), int(n), causal) for n in lens)
+        flop = sum(flops(1, h, int(n), int(n), causal) for n in lens)
         res["causal" if causal else "dense"] = measure(f"varlen causal={causal}", fn, o, checks, flop)
     out["varlen"] = res
     del q, k, v, o
@@ -715,7 +773,7 @@ def headline(torch, orc, runner, args, b, h, s, stream, pairs, spin_ms=0.0, obse
         samples, tel = timed_with_telemetry(
             lambda: time_graph(torch, fn, args.steps, args.warmup, observations or args.observations, stream,
                                spin_ms=spin_ms))
-        flop = orc.flops(b, h, s, s, causal)
+        flop = flops(b, h, s, s, causal)
         us = statistics.mean(samples)
         out[causal] = dict(us=us, median_us=statistics.median(samples), samples_us=samples,
                            tflops=flop / us / 1e6, flop=flop, check=check, check_lse=check_lse, telemetry=tel)
@@ -741,6 +799,9 @@ def main():
     runner = pkg.Runner()
     if args.pmc_pass:
         pmc_pass(torch, runner, args)
+        return
+    if args.mfma_ceiling:
+        mfma_ceiling(torch, runner, pkg, args)
         return
 
     b, h, s = args.batch, args.heads, args.seq

@@ -33,6 +33,7 @@ HIPCC_FLAGS = [
     "-Rpass-analysis=kernel-resource-usage",
 ]
 KAT_LIB_PATH = ROOT / "build" / "libfav4_loader_kat.so"
+CEILING_LIB_PATH = ROOT / "build" / "libfav4_mfma_ceiling.so"
 RESOURCE_LOG = ROOT / "build" / "resource-usage.txt"
 MANIFEST = ROOT / "build" / "build-manifest.json"
 
@@ -80,9 +81,11 @@ def parse_resource_usage(text: str) -> dict:
 
 
 def build_library(out: Path = LIB_PATH, verbose: bool = False) -> Path:
-    """Compile ``csrc/bshd.hip`` for gfx950 into ``build/libfav4_bshd.so`` and
-    the loader probe ``csrc/loader_kat.hip`` into ``build/libfav4_loader_kat.so``
-    (a test library), keep the compiler's kernel-resource-usage remarks in
+    """Compile ``csrc/bshd.hip`` for gfx950 into ``build/libfav4_bshd.so``, the
+    loader probe ``csrc/loader_kat.hip`` into ``build/libfav4_loader_kat.so``
+    (a test library) and the MFMA-only probe ``csrc/mfma_ceiling.hip`` into
+    ``build/libfav4_mfma_ceiling.so`` (a measurement library, read by
+    ``bench.py --mfma-ceiling``), keep the compiler's kernel-resource-usage remarks in
     ``build/resource-usage.txt`` and write ``build/build-manifest.json``
     (toolchain, flags, source and library sha256, per-kernel resources)."""
     import hashlib
@@ -91,7 +94,8 @@ def build_library(out: Path = LIB_PATH, verbose: bool = False) -> Path:
     import time
     out.parent.mkdir(parents=True, exist_ok=True)
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    jobs = {out: CSRC / "bshd.hip", KAT_LIB_PATH: CSRC / "loader_kat.hip"}
+    jobs = {out: CSRC / "bshd.hip", KAT_LIB_PATH: CSRC / "loader_kat.hip",
+            CEILING_LIB_PATH: CSRC / "mfma_ceiling.hip"}
     procs = {}
     for lib, src in jobs.items():
         tmp = lib.with_suffix(".so.tmp")

@@ -310,3 +310,14 @@ def test_bottom_right_reference_matches_direct_loop():
                 p = np.exp(sc - m)
                 assert np.allclose(o[0, i, hh], (p[:, None] * vf[:lim + 1, hh]).sum(0) / p.sum(), atol=1e-9)
                 assert abs(lse[0, hh, i] - (m + np.log(p.sum()))) < 1e-9
+
+
+def test_bench_flop_count_matches_the_oracles():
+    """bench.py counts FLOPs itself (its timed legs call nothing under
+    oracle/); the count must be the oracle's on dense, causal, Sq > Sk and
+    Sq < Sk shapes."""
+    import itertools
+    import bench
+    for b, h, sq, sk, causal in itertools.product([1, 3], [1, 8], [1, 100, 257, 4096], [1, 64, 3077, 4096],
+                                                 [False, True]):
+        assert bench.flops(b, h, sq, sk, causal) == orc.flops(b, h, sq, sk, causal), (b, h, sq, sk, causal)
