@@ -714,3 +714,24 @@ def test_noalloc_rejects_plans_past_its_array(lib, Args):
         assert lib.fav4_bshd_forward_splitkv_gqa_noalloc(C.byref(a), kvh, causal, splits, None) == \
             HIP_ERROR_INVALID_VALUE, (kvh, causal, splits)
     assert lib.fav4_bshd_forward_splitkv_gqa_noalloc(None, 8, 0, 0, None) == HIP_ERROR_INVALID_VALUE
+
+
+def test_mfma_ceiling_probe_library():
+    """The measurement library behind `bench.py --mfma-ceiling` exports its one
+    entry point and rejects arguments outside its ranges before any HIP call."""
+    import ctypes as C
+    import subprocess
+    pkg = load_package()
+    if not pkg.CEILING_LIB_PATH.exists():
+        pkg.build_library()
+    syms = subprocess.run(["nm", "-D", "--defined-only", str(pkg.CEILING_LIB_PATH)], capture_output=True,
+                          text=True, check=True).stdout
+    assert sorted(ln.split()[-1] for ln in syms.splitlines() if " T " in ln) == ["fav4_probe_mfma_ceiling"]
+    import torch  # noqa: F401  (torch's HIP runtime first, as the package's loader does)
+    probe = C.CDLL(str(pkg.CEILING_LIB_PATH))
+    probe.fav4_probe_mfma_ceiling.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    probe.fav4_probe_mfma_ceiling.restype = C.c_int
+    for shape, grid, iters, out in [(2, 256, 16, 0x1000), (-1, 256, 16, 0x1000), (0, 0, 16, 0x1000),
+                                    (0, 65537, 16, 0x1000), (0, 256, 0, 0x1000), (1, 256, (1 << 20) + 1, 0x1000),
+                                    (0, 256, 16, None), (1, 256, 16, 0x1002)]:
+        assert probe.fav4_probe_mfma_ceiling(shape, grid, iters, out, None) == 1, (shape, grid, iters, out)
