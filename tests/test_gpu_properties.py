@@ -18,6 +18,15 @@ Sq=Sk=4096 D128), checked on every output element without the oracle.
   bitwise the contiguous call's and finite. A NaN reaching a masked PV
   product would show, since 0 * NaN = NaN. The O rows past sq keep their
   sentinel.
+* The other entry points, each on one exact property:
+  - constant V through the GQA forward (B32 H8, 2 K/V heads, S4096);
+  - constant V through split-KV with Auto chunks: the bench's split-KV
+    prefill (B1 H8 Sq1024 Sk32768, dense and causal), its GQA decode
+    (B4 H32 with 8 K/V heads, one query against 32768 keys) and a
+    single-head causal prefill of 16384 tokens;
+  - independence of the sequences of the bench's packed batch (32
+    sequences of 1237-6743 tokens): rewriting one leaves the others' O
+    and LSE bitwise unchanged, dense, top-left and bottom-right causal.
 """
 import pytest
 
@@ -120,3 +129,87 @@ def test_nan_rows_past_the_tails_are_never_used(gpu_runner, causal, config):
     assert _same(torch, o_full[:, :s], o_ref)
     assert _same(torch, lse, l_ref)
     assert (o_full[:, s:] == 7.0).all().item(), "rows past sq were written"
+
+
+# The other entry points, each on one exact property.
+
+def _const_v(torch, b, s, kvh, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    c = torch.randn((b, 1, kvh, 128), device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
+    return c, c.expand(b, s, kvh, 128).contiguous()
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["dense", "causal"])
+def test_constant_values_gqa(gpu_runner, causal):
+    """B32 H8 with 2 K/V heads, S4096: every query head gets its K/V head's row."""
+    import torch
+    kvh = 2
+    q, _, _ = _inputs(torch, B, H, S, S, seed=501)
+    _, k, _ = _inputs(torch, B, kvh, S, S, seed=502)
+    c, v = _const_v(torch, B, S, kvh, seed=503)
+    print(f"  constant V gqa B{B} H{H} KVH{kvh} S{S} causal={causal}", flush=True)
+    o = torch.full_like(q, float("nan"))
+    gpu_runner.call_gqa(q, k, v, o, None, causal, 0)
+    torch.cuda.synchronize()
+    want = c.repeat_interleave(H // kvh, dim=2).expand_as(o)
+    assert _same(torch, o, want)
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 8, 1024, 32768, False), (1, 8, 8, 1024, 32768, True),
+                                   (4, 32, 8, 1, 32768, False), (1, 1, 1, 16384, 16384, True)],
+                         ids=["prefill_dense", "prefill_causal", "gqa_decode", "single_head_causal"])
+def test_constant_values_splitkv(gpu_runner, shape):
+    """Split-KV with Auto chunks (the bench's split-KV and decode shapes): the
+    FP32 chunk partials and their merge reproduce the constant row exactly."""
+    import torch
+    b, h, kvh, sq, sk, causal = shape
+    q, _, _ = _inputs(torch, b, h, sq, sq, seed=601)
+    _, k, _ = _inputs(torch, b, kvh, sk, sk, seed=602)
+    c, v = _const_v(torch, b, sk, kvh, seed=603)
+    splits = gpu_runner.splitkv_select(b, h, sq, sk, causal, kv_heads=kvh)
+    print(f"  constant V split-KV B{b} H{h} KVH{kvh} {sq}x{sk} causal={causal} splits={splits}", flush=True)
+    o = torch.full_like(q, float("nan"))
+    lse = torch.full((b, h, sq), float("nan"), device="cuda", dtype=torch.float32)
+    gpu_runner.call_splitkv(q, k, v, o, lse, causal, 0)
+    torch.cuda.synchronize()
+    assert _same(torch, o, c.repeat_interleave(h // kvh, dim=2).expand_as(o))
+    assert torch.isfinite(lse).all().item()
+
+
+@pytest.mark.parametrize("causal", [0, 1, 2], ids=["dense", "causal", "bottom_right"])
+def test_varlen_sequences_are_independent(gpu_runner, causal):
+    """The bench's packed batch (32 sequences of 1237-6743 tokens, H8):
+    rewriting one sequence's Q/K/V leaves every other sequence's O and LSE
+    bitwise unchanged."""
+    import numpy as np
+    import torch
+    lens = np.random.default_rng(11939).integers(S // 4, 7 * S // 4 + 1, size=B)
+    cu_h = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    total, maxlen = int(cu_h[-1]), int(lens.max())
+    cu = torch.from_numpy(cu_h).cuda()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(701)
+    mk = lambda: torch.randn((total, H, 128), device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
+    q, k, v = mk(), mk(), mk()
+    sel = 7
+    a, e = int(cu_h[sel]), int(cu_h[sel + 1])
+    print(f"  varlen independence {B} sequences ({total} tokens) causal={causal} rewrite sequence {sel}", flush=True)
+
+    def run(q, k, v):
+        o = torch.full_like(q, float("nan"))
+        lse = torch.full((H, total), float("nan"), device="cuda", dtype=torch.float32)
+        gpu_runner.call_varlen(q, k, v, o, lse, cu, cu, maxlen, maxlen, causal)
+        torch.cuda.synchronize()
+        return o, lse
+
+    o1, l1 = run(q, k, v)
+    q2, k2, v2 = q.clone(), k.clone(), v.clone()
+    for x in (q2, k2, v2):
+        x[a:e] = torch.randn(x[a:e].shape, device="cuda", generator=g).to(torch.bfloat16)
+    o2, l2 = run(q2, k2, v2)
+    keep = torch.ones(total, dtype=torch.bool, device="cuda")
+    keep[a:e] = False
+    assert _same(torch, o1[keep], o2[keep])
+    assert _same(torch, l1[:, keep], l2[:, keep])
+    assert not _same(torch, o1[a:e], o2[a:e])
