@@ -238,13 +238,23 @@ def cpu_info():
             info["bios_model"] = val
         elif key == "Socket(s)":
             info["sockets"] = int(val) if val.isdigit() else val
-    if not info["model"]:
-        try:
-            with open("/proc/cpuinfo") as f:
-                info["model"] = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
-                                     None)
-        except OSError:
-            pass
+    # /proc/cpuinfo's identification of the first core: a virtual machine's
+    # model name can be as short as "AMD EPYC", and family / model / stepping
+    # still name the part.
+    try:
+        with open("/proc/cpuinfo") as f:
+            first = {}
+            for ln in f:
+                if not ln.strip():
+                    break
+                key, _, val = ln.partition(":")
+                first[key.strip()] = val.strip()
+        if not info["model"]:
+            info["model"] = first.get("model name")
+        info["cpuinfo"] = {k: first.get(k) for k in ("model name", "cpu family", "model", "stepping", "cpu MHz",
+                                                       "cache size")}
+    except OSError:
+        pass
     return info
 
 
@@ -304,7 +314,7 @@ def cpu_baseline(torch, orc, q, k, v, budget_s):
                 fp32=dict(value=round(flop1 * done32 / elapsed32 / 1e12, 4), unit="TFLOP/s",
                           sample=f"FP32 numpy textbook attention, {done32} slices in {elapsed32:.1f} s"),
                 cpu_model=host.get("model"), bios_model=host.get("bios_model"), sockets=host.get("sockets"),
-                affinity_cores=affinity)
+                affinity_cores=affinity, cpuinfo=host.get("cpuinfo"))
 
 
 def time_eager(torch, fn, steps, warmup, stream):
