@@ -24,6 +24,8 @@ Sq=Sk=4096 D128), checked on every output element without the oracle.
     prefill (B1 H8 Sq1024 Sk32768, dense and causal), its GQA decode
     (B4 H32 with 8 K/V heads, one query against 32768 keys) and a
     single-head causal prefill of 16384 tokens;
+  - constant V through the bench's packed and paged decode batch (32
+    sequences x 1 query, 1949-31077 keys), dense and bottom-right causal;
   - independence of the sequences of the bench's packed batch (32
     sequences of 1237-6743 tokens): rewriting one leaves the others' O
     and LSE bitwise unchanged, dense, top-left and bottom-right causal.
@@ -213,3 +215,51 @@ def test_varlen_sequences_are_independent(gpu_runner, causal):
     assert _same(torch, o1[keep], o2[keep])
     assert _same(torch, l1[:, keep], l2[:, keep])
     assert not _same(torch, o1[a:e], o2[a:e])
+
+
+@pytest.mark.parametrize("causal", [0, 2], ids=["dense", "bottom_right"])
+def test_constant_values_packed_and_paged_decode(gpu_runner, causal):
+    """The bench's continuous-batching decode (32 sequences x 1 query, cache
+    lengths 1949-31077, H32 with 8 K/V heads, Auto chunks): with every V row
+    of a K/V head equal, every output row is that row, contiguous and from
+    64-key pages in random order."""
+    import numpy as np
+    import torch
+    vb, vh, vkvh, ps = 32, 32, 8, 64
+    klens = np.random.default_rng(4242).integers(1024, 32768 + 1, size=vb)
+    cuk_h = np.concatenate([[0], np.cumsum(klens)]).astype(np.int32)
+    tk, maxk = int(cuk_h[-1]), int(klens.max())
+    cuq = torch.arange(vb + 1, dtype=torch.int32, device="cuda")
+    cuk = torch.from_numpy(cuk_h).cuda()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(801)
+    q = torch.randn((vb, vh, 128), device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn((tk, vkvh, 128), device="cuda", generator=g).to(torch.bfloat16)
+    c = torch.randn((1, vkvh, 128), device="cuda", generator=g).to(torch.bfloat16)
+    v = c.expand(tk, vkvh, 128).contiguous()
+    want = c.repeat_interleave(vh // vkvh, dim=1).expand(vb, vh, 128)
+    print(f"  constant V packed decode {vb} sequences, {tk} keys, causal={causal}", flush=True)
+    o = torch.full_like(q, float("nan"))
+    gpu_runner.call_splitkv_varlen(q, k, v, o, None, cuq, cuk, 1, maxk, causal)
+    torch.cuda.synchronize()
+    assert _same(torch, o, want), "packed decode"
+
+    npg = [-(-int(n) // ps) for n in klens]
+    perm = torch.randperm(sum(npg), generator=torch.Generator().manual_seed(5)).cuda()
+    kc = torch.zeros((sum(npg), ps, vkvh, 128), device="cuda", dtype=torch.bfloat16)
+    vc = c.expand(sum(npg), ps, vkvh, 128).contiguous()
+    table = torch.zeros((vb, max(npg)), device="cuda", dtype=torch.int32)
+    at = 0
+    for i, n in enumerate(npg):
+        ids = perm[at:at + n]
+        at += n
+        table[i, :n] = ids.to(torch.int32)
+        ks, ke = int(cuk_h[i]), int(cuk_h[i + 1])
+        pad = torch.zeros((n * ps, vkvh, 128), device="cuda", dtype=torch.bfloat16)
+        pad[:ke - ks] = k[ks:ke]
+        kc[ids] = pad.view(n, ps, vkvh, 128)
+    seqlens = torch.from_numpy(klens.astype(np.int32)).cuda()
+    o.fill_(float("nan"))
+    gpu_runner.call_splitkv_paged(q, kc, vc, o, None, cuq, seqlens, table, 1, maxk, 0, total_k=tk, causal=causal)
+    torch.cuda.synchronize()
+    assert _same(torch, o, want), "paged decode"
