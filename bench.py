@@ -11,18 +11,26 @@ launch stream; six such observations are taken and the mean is reported.  The
 FLOP convention is the reference's (bshd.py:169-170, README.md:59): useful
 QK+PV only, dense 4*B*H*D*S^2, causal 4*B*H*D*S(S+1)/2.
 
-Before timing, each timed output is checked against the FP64 oracle on the
-reference's sampled rows (bshd.py:147-148) for a subset of (b, h) pairs.
+Every timed shape is first checked against the FP64 oracle on the
+reference's sampled rows (bshd.py:147-148) for three (b, h) pairs, with and
+without the LSE output.
+
+The long-sequence sweep (B and H of the headline, S in 512..32768, dense and
+causal) times this library against torch's scaled_dot_product_attention (its
+fused flash backend, else its memory-efficient one; never the unfused math
+path) on the same device and inputs the way the reference times itself
+against CK (bshd.py:151-166): both are graph-captured, and their observations
+interleave in the order ABBA BAAB ABBA, six each.  The headline shape gets
+the same comparison after its own dedicated timing.
 
 The ``cpu_baseline`` leg times the FP64 oracle on this host's cores on a
 bounded sample of (b, h) slices of the same dense workload (a baseline only).
 
-The ``comparator`` leg times torch's scaled_dot_product_attention on the same
-device and inputs (contiguous BHSD copies, its fused flash backend, else its
-memory-efficient one; never the unfused math path), interleaved with this
-library's kernel in A-B-B-A order, and reports the speedup and the largest
-difference between the two outputs.  ``provenance`` records what was measured:
-library and source hashes, toolchain and torch versions, device and clocks.
+Output: stdout ends with ONE short JSON line (the driver's record; kept well
+under 4 KB), the same way the reference prints one summary line per shape
+and keeps bulky records for its --output file (bshd.py:183-185).  The full
+record (checks, telemetry, provenance and build manifest, every sample) goes
+to the --detail file.  Progress lines go to stderr, prefixed with '#'.
 """
 from __future__ import annotations
 
@@ -40,13 +48,17 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+METRIC = "fwd TFLOP/s + % BF16 MFMA peak, B32 H8 D128 S4096 dense & causal"
 PEAK_BF16_TFLOPS = 2516.6      # MI355X dense BF16 MFMA: 256 CU x 4 SIMD x 1024 FLOP/clk x 2.4 GHz
 HBM_TBPS = 8.0
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_fmha_fwd_dense_b32h8s4096.md"
-SWEEP_SPIN_MS = 50.0           # untimed spin-up before each sweep shape (report-only rows)
+SWEEP_SPIN_MS = 50.0           # untimed spin-up before each sweep shape
+DEFAULT_SWEEP = "512,1024,2048,8192,16384,32768"   # bshd.py:195 plus the long-sequence configs
+ABBA = "ABBABAABABBA"          # bshd.py:151-166: six observations of each side
+LINE_LIMIT = 4096              # bytes of the final stdout line
 
 
-def parse_args():
+def parse_args(argv=None):
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
@@ -60,12 +72,15 @@ def parse_args():
     p.add_argument("--no-check", action="store_true", help="skip the sampled-row FP64 check")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
-    p.add_argument("--sweep", default="512,1024,8192,16384,32768",
+    p.add_argument("--sweep", default=DEFAULT_SWEEP,
                    help="comma list of the long-sequence sweep's lengths (B and H as the headline; dense and causal)")
     p.add_argument("--no-sweep", action="store_true", help="skip the long-sequence sweep")
     p.add_argument("--no-comparator", action="store_true", help="skip the torch SDPA comparator")
-    p.add_argument("--no-splitkv", action="store_true", help="skip the split-KV report (B1 H8 Sq1024 Sk32768; B1 H1 S16384 causal)")
-    p.add_argument("--no-api", action="store_true", help="skip the GQA / varlen report")
+    p.add_argument("--splitkv", action="store_true",
+                   help="also time the split-KV entry point (B1 H8 Sq1024 Sk32768; B1 H1 S16384 causal)")
+    p.add_argument("--api", action="store_true", help="also time the GQA / varlen / decode entry points")
+    p.add_argument("--detail", default=str(ROOT / "gpurun_out" / "bench_detail.json"),
+                   help="file for the full record (checks, telemetry, provenance, samples)")
     p.add_argument("--no-telemetry", action="store_true",
                    help="start no child processes (amd-smi clocks, hipcc version), e.g. under a profiler")
     p.add_argument("--mfma-ceiling", action="store_true",
@@ -75,72 +90,16 @@ def parse_args():
     p.add_argument("--pmc-pass", action="store_true",
                    help="profiling mode for counter runs: two eager launches per mask type, then a "
                         "plain 1 GiB device copy (HBM counter calibration); prints no JSON")
-    return p.parse_args()
+    return p.parse_args(argv)
 
 
-def pmc_pass(torch, runner, args):
-    """Eager launches for rocprofv3 --pmc runs (no graphs, one dispatch per launch)."""
-    b, h, s = args.batch, args.heads, args.seq
-    q, k, v = make_inputs(torch, b, h, s)
-    o = torch.empty_like(q)
-    for causal in (False, True):
-        for _ in range(2):
-            runner.call(q, k, v, o, None, causal, args.config)
-        torch.cuda.synchronize()
-        print(f"# pmc-pass launched B{b} H{h} S{s} causal={causal} x2", flush=True)
-    del q, k, v, o
-    src = torch.ones(1 << 28, device="cuda", dtype=torch.float32)    # 1 GiB
-    dst = torch.empty_like(src)
-    for _ in range(2):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    print("# pmc-pass copy: 1073741824 bytes read + 1073741824 bytes written per dispatch", flush=True)
+def log(msg):
+    print(f"# {msg}", file=sys.stderr, flush=True)
 
 
-def mfma_ceiling(torch, runner, pkg, args):
-    """The MFMA rate with nothing else on the chip (libfav4_mfma_ceiling.so,
-    built by build()), at the clock the board's power limit allows, beside
-    the headline kernels measured the same way. One workgroup of 8 waves per
-    CU streams BF16 MFMAs on pseudo-random register operands; shape 0 is
-    32x32x16 (the forward's), shape 1 16x16x32 at equal FLOPs."""
-    import ctypes as C
-    lib = C.CDLL(str(pkg.CEILING_LIB_PATH))
-    lib.fav4_probe_mfma_ceiling.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
-    lib.fav4_probe_mfma_ceiling.restype = C.c_int
-    stream = torch.cuda.Stream()
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    iters = 2048                                   # about 2 ms per launch
-    out = torch.empty(cus * 512, device="cuda", dtype=torch.float32)
-    res = {}
-    for shape, name in ((0, "mfma_32x32x16"), (1, "mfma_16x16x32")):
-        fn = lambda: lib.fav4_probe_mfma_ceiling(shape, cus, iters, out.data_ptr(), stream.cuda_stream)
-        with torch.cuda.stream(stream):
-            st = fn()
-        torch.cuda.synchronize()
-        if st:
-            raise SystemExit(f"mfma ceiling probe: HIP status {st}")
-        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
-        flop = cus * 8 * iters * 1048576
-        res[name] = dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1),
-                         frac_of_peak=round(flop / us / 1e6 / PEAK_BF16_TFLOPS, 4),
-                         telemetry_under_load=loaded_telemetry(torch, fn, stream) if _TELEMETRY else None)
-        print(f"# {name}: {us:.1f} us, {flop / us / 1e6:.1f} TFLOP/s", file=sys.stderr, flush=True)
-    b, h, s = args.batch, args.heads, args.seq
-    q, k, v = make_inputs(torch, b, h, s)
-    o = torch.empty_like(q)
-    for causal in (False, True):
-        fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
-        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
-        tflops = flops(b, h, s, s, causal) / us / 1e6
-        res["fwd_causal" if causal else "fwd_dense"] = dict(
-            us=round(us, 2), tflops=round(tflops, 1), frac_of_peak=round(tflops / PEAK_BF16_TFLOPS, 4),
-            telemetry_under_load=loaded_telemetry(torch, fn, stream) if _TELEMETRY else None)
-        print(f"# B{b} H{h} S{s} causal={causal}: {us:.1f} us, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
-    res["fwd_dense_of_ceiling"] = round(res["fwd_dense"]["tflops"] / res["mfma_32x32x16"]["tflops"], 4)
-    print(json.dumps({"mode": "mfma_ceiling", "workload": f"B{b} H{h} Sq=Sk={s} D128 BF16, LSE off, config "
-                      f"{args.config}", "cus": cus, "iters_per_wave": iters, **res}), flush=True)
-
-
+# ---------------------------------------------------------------------------
+# FLOPs, bytes, inputs, checks
+# ---------------------------------------------------------------------------
 def flops(b, h, sq, sk, causal):
     """Useful QK+PV FLOPs, the reference's convention (benchmarks/bshd.py:169-170):
     4*B*H*128*Sq*Sk dense; top-left causal counts the keys each row sees,
@@ -149,6 +108,19 @@ def flops(b, h, sq, sk, causal):
         return 4 * b * h * 128 * sq * sk
     full = min(sq, sk)
     return 4 * b * h * 128 * (full * (full + 1) // 2 + max(0, sq - sk) * sk)
+
+
+def compulsory_bytes(b, h, sq, sk, lse=False):
+    """HBM bytes every implementation must move: Q and O ([B,Sq,H,128] BF16),
+    K and V ([B,Sk,H,128] BF16), and the FP32 LSE when written."""
+    return 2 * b * h * 128 * (2 * sq + 2 * sk) + (4 * b * h * sq if lse else 0)
+
+
+def roofline_floor_us(b, h, sq, sk, causal):
+    """The shape's roofline time: max(MFMA time at the nominal peak, compulsory
+    bytes at 8 TB/s), in microseconds."""
+    return max(flops(b, h, sq, sk, causal) / (PEAK_BF16_TFLOPS * 1e6),
+               compulsory_bytes(b, h, sq, sk) / (HBM_TBPS * 1e6))
 
 
 def make_inputs(torch, b, h, s, seed=11939):
@@ -186,12 +158,39 @@ def check_rows(torch, orc, q, k, v, o, causal, pairs, lse=None):
     return orc.errors(np.stack(gots), np.stack(got_l), np.stack(refs), np.stack(ref_l)), rows
 
 
-def time_graph(torch, fn, steps, warmup, observations, stream, spin_ms=0.0):
-    """Per-launch microseconds from HIP-graph replays bracketed by events on `stream`.
+def run_once(torch, fn, stream):
+    with torch.cuda.stream(stream):
+        fn()
+    torch.cuda.synchronize()
 
-    spin_ms > 0: before the observations, replay the warmup graph (untimed)
-    until that much wall time has passed, so that short launches are timed at
-    the loaded clock rather than while the GPU ramps up from idle."""
+
+def checked(torch, orc, runner, q, k, v, o, causal, config, stream, pairs, what):
+    """Sampled-row FP64 checks of one shape, without and with the LSE output
+    (benchmarks/bshd.py:147-156 checks every timed shape both ways).  Raises
+    when either misses the acceptance bar; returns both error dicts."""
+    b, s, h, _ = q.shape
+    o.fill_(float("nan"))
+    torch.cuda.synchronize()   # the fill runs on the default stream
+    run_once(torch, lambda: runner.call(q, k, v, o, None, causal, config, stream=stream.cuda_stream), stream)
+    e, _ = check_rows(torch, orc, q, k, v, o, causal, pairs)
+    if not orc.check_acceptance_tolerance(e):
+        raise SystemExit(f"sampled-row check failed ({what} causal={causal}): {e}")
+    lse = torch.full((b, h, s), float("nan"), device=q.device, dtype=torch.float32)
+    o.fill_(float("nan"))
+    torch.cuda.synchronize()
+    run_once(torch, lambda: runner.call(q, k, v, o, lse, causal, config, stream=stream.cuda_stream), stream)
+    e_lse, _ = check_rows(torch, orc, q, k, v, o, causal, pairs, lse=lse)
+    del lse
+    if not orc.check_acceptance_tolerance(e_lse):
+        raise SystemExit(f"sampled-row LSE check failed ({what} causal={causal}): {e_lse}")
+    return e, e_lse
+
+
+# ---------------------------------------------------------------------------
+# Timing (benchmarks/bshd.py:34-51, 151-166)
+# ---------------------------------------------------------------------------
+def capture(torch, fn, steps, warmup, stream):
+    """(warmup graph, timed graph) of `warmup` and `steps` launches of fn on `stream`."""
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         g_timed = torch.cuda.CUDAGraph()
@@ -202,28 +201,134 @@ def time_graph(torch, fn, steps, warmup, observations, stream, spin_ms=0.0):
         with torch.cuda.graph(g_warm, stream=stream):
             for _ in range(warmup):
                 fn()
-    if spin_ms > 0:
-        t_end = time.perf_counter() + spin_ms / 1000.0
-        while time.perf_counter() < t_end:
-            with torch.cuda.stream(stream):
-                g_warm.replay()
-            torch.cuda.synchronize()
-    samples = []
-    for _ in range(observations):
+    torch.cuda.synchronize()
+    return g_warm, g_timed
+
+
+def spin(torch, g_warm, stream, spin_ms):
+    """Replay the warmup graph (untimed) until spin_ms of wall time has passed,
+    so short launches are timed at the loaded clock, not while the GPU ramps
+    up from idle."""
+    t_end = time.perf_counter() + spin_ms / 1000.0
+    while time.perf_counter() < t_end:
         with torch.cuda.stream(stream):
             g_warm.replay()
-            torch.cuda.synchronize()
-            start = torch.cuda.Event(enable_timing=True)
-            end = torch.cuda.Event(enable_timing=True)
-            start.record(stream)
-            g_timed.replay()
-            end.record(stream)
-        end.synchronize()
-        samples.append(start.elapsed_time(end) * 1000.0 / steps)
+        torch.cuda.synchronize()
+
+
+def observe(torch, graphs, steps, stream):
+    """One observation: replay the warmup graph, then the timed graph between
+    two events on `stream`; microseconds per launch."""
+    g_warm, g_timed = graphs
+    with torch.cuda.stream(stream):
+        g_warm.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        g_timed.replay()
+        end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) * 1000.0 / steps
+
+
+def time_graph(torch, fn, steps, warmup, observations, stream, spin_ms=0.0):
+    """Per-launch microseconds of `observations` graph observations of fn."""
+    graphs = capture(torch, fn, steps, warmup, stream)
+    if spin_ms > 0:
+        spin(torch, graphs[0], stream, spin_ms)
+    samples = [observe(torch, graphs, steps, stream) for _ in range(observations)]
+    del graphs
     torch.cuda.synchronize()
     return samples
 
 
+def time_interleaved(torch, fa, fb, steps, warmup, stream, spin_ms=0.0, order=ABBA):
+    """Graph-timed A and B with their observations interleaved in `order`
+    (the reference's ABBA BAAB ABBA against CK, bshd.py:151-166)."""
+    ga = capture(torch, fa, steps, warmup, stream)
+    gb = capture(torch, fb, steps, warmup, stream)
+    if spin_ms > 0:
+        spin(torch, ga[0], stream, spin_ms / 2)
+        spin(torch, gb[0], stream, spin_ms / 2)
+    out = {"A": [], "B": []}
+    for who in order:
+        out[who].append(observe(torch, ga if who == "A" else gb, steps, stream))
+    del ga, gb
+    torch.cuda.synchronize()
+    return out["A"], out["B"]
+
+
+def sweep_launches(s, steps, warmup):
+    """Launches per timed / warmup graph at sequence length s: the reference's
+    20 / 5 up to S8192; fewer for the longest shapes (one S32768 dense launch
+    takes about 0.12 s), so the interleaved comparison stays within a minute."""
+    if s >= 32768:
+        return min(steps, 3), min(warmup, 1)
+    if s >= 16384:
+        return min(steps, 6), min(warmup, 2)
+    return steps, warmup
+
+
+# ---------------------------------------------------------------------------
+# Comparator: torch SDPA on the same device
+# ---------------------------------------------------------------------------
+def sdpa_backend(torch):
+    """The first fused SDPA backend that runs here (flash, else
+    memory-efficient), as (name, backend enum), or None."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    x = torch.zeros((1, 1, 256, 128), device="cuda", dtype=torch.bfloat16)
+    for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel([be]):
+                F.scaled_dot_product_attention(x, x, x, scale=1.0 / math.sqrt(128))
+            torch.cuda.synchronize()
+            return name, be
+        except RuntimeError:
+            continue
+    return None
+
+
+class Sdpa:
+    """torch SDPA over contiguous BHSD copies of Q/K/V (its preferred layout;
+    the copies are not timed)."""
+
+    def __init__(self, torch, backend, q, k, v):
+        import torch.nn.functional as F
+        from torch.nn.attention import sdpa_kernel
+        self.F, self.sdpa_kernel, self.backend = F, sdpa_kernel, backend
+        self.qh, self.kh, self.vh = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+        self.out = None
+
+    def __call__(self, causal):
+        with self.sdpa_kernel([self.backend[1]]):
+            self.out = self.F.scaled_dot_product_attention(self.qh, self.kh, self.vh, is_causal=causal,
+                                                           scale=1.0 / math.sqrt(128))
+
+    def max_diff(self, torch, o, rows):
+        """Largest |SDPA - ours| over the sampled rows (BSHD)."""
+        rt = torch.from_numpy(rows).to(o.device)
+        theirs = self.out.index_select(2, rt).transpose(1, 2).float()
+        return (theirs - o.index_select(1, rt).float()).abs().max().item()
+
+
+def compare(torch, orc, runner, sdpa, q, k, v, o, causal, config, stream, steps, warmup, spin_ms):
+    """Ours (A) against SDPA (B), graph-timed and interleaved; plus the largest
+    output difference on the sampled rows."""
+    ours = lambda: runner.call(q, k, v, o, None, causal, config, stream=stream.cuda_stream)
+    theirs = lambda: sdpa(causal)
+    run_once(torch, theirs, stream)   # lazy init outside the capture
+    a, bs = time_interleaved(torch, ours, theirs, steps, warmup, stream, spin_ms=spin_ms)
+    run_once(torch, ours, stream)
+    run_once(torch, theirs, stream)
+    diff = sdpa.max_diff(torch, o, orc.sample_rows(q.shape[1]))
+    return a, bs, diff
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline
+# ---------------------------------------------------------------------------
 def cpu_info():
     """Host CPU description: lscpu's model name (else /proc/cpuinfo's), sockets,
     and the cores this process may run on."""
@@ -306,86 +411,25 @@ def cpu_baseline(torch, orc, q, k, v, budget_s):
     flop1 = flops(1, 1, s, s, False)
     host = cpu_info()
     return dict(value=flop1 * done / elapsed / 1e12, unit="TFLOP/s", cores=cores, kind="port",
-                sample=f"FP64 numpy oracle, {done} of {len(pairs)} (b,h) slices of B{b} H{h} "
-                       f"S{s} D{d} dense, {elapsed:.1f} s on {cores} threads (one slice per thread, "
-                       f"single-threaded BLAS; {affinity} cores in the affinity set, threads capped by "
-                       f"OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'unset')}); extrapolated "
-                       f"whole-job time {elapsed * len(pairs) / done:.1f} s",
+                sample=f"FP64 numpy oracle on {done} of {len(pairs)} (b,h) slices of the dense B{b} H{h} S{s} "
+                       f"D{d} workload, {elapsed:.1f} s, one slice per thread",
+                slices=done, seconds=round(elapsed, 2),
+                extrapolated_whole_job_s=round(elapsed * len(pairs) / done, 1),
                 fp32=dict(value=round(flop1 * done32 / elapsed32 / 1e12, 4), unit="TFLOP/s",
                           sample=f"FP32 numpy textbook attention, {done32} slices in {elapsed32:.1f} s"),
+                threads_note=f"single-threaded BLAS; {affinity} cores in the affinity set, threads capped by "
+                             f"OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'unset')}",
                 cpu_model=host.get("model"), bios_model=host.get("bios_model"), sockets=host.get("sockets"),
                 affinity_cores=affinity, cpuinfo=host.get("cpuinfo"))
 
 
-def time_eager(torch, fn, steps, warmup, stream):
-    """Per-launch microseconds of `steps` eager launches between events on `stream`."""
-    with torch.cuda.stream(stream):
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(steps):
-            fn()
-        end.record(stream)
-    end.synchronize()
-    return start.elapsed_time(end) * 1000.0 / steps
-
-
-def comparator(torch, orc, runner, q, k, v, o, stream, args, causal_list):
-    """torch SDPA (fused backends only) vs this library on the same inputs, A-B-B-A."""
-    import torch.nn.functional as F
-    from torch.nn.attention import SDPBackend, sdpa_kernel
-    b, s, h, d = q.shape
-    qh, kh, vh = (t.transpose(1, 2).contiguous() for t in (q, k, v))
-    scale = 1.0 / math.sqrt(d)
-    backend = None
-    for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
-        try:
-            with sdpa_kernel([be]):
-                F.scaled_dot_product_attention(qh[:1, :1, :256], kh[:1, :1, :256], vh[:1, :1, :256], scale=scale)
-            torch.cuda.synchronize()
-            backend = (name, be)
-            break
-        except RuntimeError:
-            continue
-    if backend is None:
-        return None
-    out = {"name": f"torch.nn.functional.scaled_dot_product_attention, {backend[0]} backend "
-                   f"(torch {torch.__version__})",
-           "layout": "contiguous BHSD copies of the same Q/K/V (its preferred layout; copies not timed)"}
-    for causal in causal_list:
-        ref = [None]
-
-        def theirs():
-            with sdpa_kernel([backend[1]]):
-                ref[0] = F.scaled_dot_product_attention(qh, kh, vh, is_causal=causal, scale=scale)
-
-        ours = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
-        t = {"ours": [], "theirs": []}
-        for who in ("ours", "theirs", "theirs", "ours"):
-            t[who].append(time_eager(torch, ours if who == "ours" else theirs, args.steps, args.warmup, stream))
-        torch.cuda.synchronize()
-        diff = (ref[0].transpose(1, 2).float() - o.float()).abs().max().item()
-        flop = flops(b, h, s, s, causal)
-        us_o, us_t = statistics.mean(t["ours"]), statistics.mean(t["theirs"])
-        out["causal" if causal else "dense"] = dict(
-            tflops=round(flop / us_t / 1e6, 2), us_per_launch=round(us_t, 3),
-            ours_tflops_eager=round(flop / us_o / 1e6, 2), speedup=round(us_t / us_o, 4),
-            max_abs_diff_vs_ours=round(diff, 5))
-        print(f"# comparator causal={causal}: SDPA {flop / us_t / 1e6:.1f} TFLOP/s, ours {flop / us_o / 1e6:.1f} "
-              f"(eager, ABBA), speedup {us_t / us_o:.3f}, max|diff| {diff:.4f}", file=sys.stderr, flush=True)
-    del qh, kh, vh
-    return out
-
-
+# ---------------------------------------------------------------------------
+# Opt-in reports of the other entry points (split-KV, GQA, varlen, decode)
+# ---------------------------------------------------------------------------
 def splitkv_report(torch, orc, runner, args, stream):
     """Few (b, h, q tile) items and long keys: the single-pass forward against the
     split-KV forward (Auto chunk count), both graph-timed, each output checked on
-    sampled rows first.  B1 H8 Sq1024 Sk32768 dense and causal (causal rows see
-    only the first 1024 keys: Auto keeps the unsplit forward there), and a
-    single-head causal prefill of 16384 tokens."""
+    sampled rows first."""
     g = torch.Generator(device="cuda")
     g.manual_seed(11939)
     out = {}
@@ -404,10 +448,8 @@ def splitkv_report(torch, orc, runner, args, stream):
                "splits": splits, "workspace_bytes": ws.numel()}
         for name, fn in (("plain", plain), ("splitkv", split)):
             o.fill_(float("nan"))
-            torch.cuda.synchronize()   # the fill runs on the default stream
-            with torch.cuda.stream(stream):
-                fn()
             torch.cuda.synchronize()
+            run_once(torch, fn, stream)
             err, _ = check_rows(torch, orc, q, k, v, o, causal, [(0, 0), (0, h - 1)])
             if not orc.check_acceptance_tolerance(err):
                 raise SystemExit(f"split-KV report: {name} check failed ({label}): {err}")
@@ -415,20 +457,17 @@ def splitkv_report(torch, orc, runner, args, stream):
             res[name] = dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1))
         res["speedup"] = round(res["plain"]["us"] / res["splitkv"]["us"], 2)
         out[label] = res
-        print(f"# splitkv B{b} H{h} {sq}x{sk} causal={causal}: plain {res['plain']['tflops']} TFLOP/s, "
-              f"split-KV ({splits} chunks) {res['splitkv']['tflops']} TFLOP/s, x{res['speedup']}",
-              file=sys.stderr, flush=True)
+        log(f"splitkv B{b} H{h} {sq}x{sk} causal={causal}: plain {res['plain']['tflops']} TFLOP/s, "
+            f"split-KV ({splits} chunks) {res['splitkv']['tflops']} TFLOP/s, x{res['speedup']}")
         del q, k, v, o, ws
     torch.cuda.empty_cache()
     return out
 
 
 def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
-    """The GQA and varlen entry points at the headline token count (B*S rows, H8):
-    GQA with `kvh` K/V heads; varlen with B ragged sequences of seeded lengths in
-    [S/4, 7S/4]; and a GQA decode through split-KV.  Graph-timed, each output
-    first checked against the FP64 oracle on sampled rows of two (sequence,
-    head) pairs of two sequences."""
+    """The GQA and varlen entry points at the headline token count (B*S rows,
+    H8), and a GQA decode through split-KV; graph-timed, each output first
+    checked against the FP64 oracle on sampled rows."""
     g = torch.Generator(device="cuda")
     g.manual_seed(11939)
     mk = lambda *shape: torch.randn(shape, device="cuda", dtype=torch.float32, generator=g).to(torch.bfloat16)
@@ -436,16 +475,14 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
 
     def measure(name, fn, o, checks, flop):
         o.fill_(float("nan"))
-        torch.cuda.synchronize()   # the fill runs on the default stream
-        with torch.cuda.stream(stream):
-            fn()
         torch.cuda.synchronize()
+        run_once(torch, fn, stream)
         for qc, kc, vc, oc, causal in checks():
             err, _ = check_rows(torch, orc, qc, kc, vc, oc, causal, [(0, 0), (0, h - 1)])
             if not orc.check_acceptance_tolerance(err):
                 raise SystemExit(f"api report: {name} check failed: {err}")
         us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream))
-        print(f"# {name}: {us:.1f} us, {flop / us / 1e6:.1f} TFLOP/s", file=sys.stderr, flush=True)
+        log(f"{name}: {us:.1f} us, {flop / us / 1e6:.1f} TFLOP/s")
         return dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1))
 
     q, k, v = mk(b, s, h, 128), mk(b, s, kvh, 128), mk(b, s, kvh, 128)
@@ -490,9 +527,7 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
     fn = lambda: runner.call_splitkv(q, k, v, o, None, False, 0, workspace=ws, stream=stream.cuda_stream)
     o.fill_(float("nan"))
     torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        fn()
-    torch.cuda.synchronize()
+    run_once(torch, fn, stream)
     grp = dh // dkvh
     for i in (0, db - 1):
         err, _ = check_rows(torch, orc, q[i:i + 1], k[i:i + 1].repeat_interleave(grp, dim=2),
@@ -502,100 +537,17 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
     us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
     kv_bytes = 2 * db * dsk * dkvh * 256
     splits = runner.splitkv_select(db, dh, 1, dsk, False, kv_heads=dkvh)
-    print(f"# gqa decode (split-KV, {splits} chunks): {us:.1f} us, K+V {kv_bytes / us / 1e6:.2f} TB/s",
-          file=sys.stderr, flush=True)
+    log(f"gqa decode (split-KV, {splits} chunks): {us:.1f} us, K+V {kv_bytes / us / 1e6:.2f} TB/s")
     out["gqa_decode"] = {"workload": f"B{db} H{dh} KV heads {dkvh} Sq=1 Sk={dsk} D128 BF16 dense, split-KV Auto",
                          "splits": splits, "us": round(us, 2), "kv_tbps": round(kv_bytes / us / 1e6, 2)}
     del q, k, v, o, ws
     torch.cuda.empty_cache()
-
-    # Continuous-batching decode: packed sequences, one new query each, ragged
-    # cache lengths; split-KV over the packed batch against the unsplit packed
-    # forward.  Reported as K+V bandwidth.
-    vb, vh, vkvh = 32, 32, 8
-    klens = np.random.default_rng(4242).integers(1024, 32768 + 1, size=vb)
-    cuk_h = np.concatenate([[0], np.cumsum(klens)]).astype(np.int32)
-    cuq_h = np.arange(vb + 1, dtype=np.int32)
-    tk, mk_len = int(cuk_h[-1]), int(klens.max())
-    cuq, cuk = torch.from_numpy(cuq_h).cuda(), torch.from_numpy(cuk_h).cuda()
-    q, k, v = mk(vb, vh, 128), mk(tk, vkvh, 128), mk(tk, vkvh, 128)
-    o = torch.empty_like(q)
-    need = runner.splitkv_varlen_workspace_size(vb, vh, vkvh, 1, mk_len, vb, tk, False)
-    ws = torch.empty(max(need, 256), device="cuda", dtype=torch.uint8)
-    splits = runner.splitkv_varlen_select(vb, vh, vkvh, 1, mk_len, vb, tk, False)
-    kv_bytes = 2 * tk * vkvh * 256
-    grp = vh // vkvh
-    res = {"workload": f"{vb} sequences x 1 query, cache lengths {int(klens.min())}..{mk_len} (seeded), {tk} keys, "
-                       f"H{vh} KV heads {vkvh} D128 BF16 dense", "splits": splits}
-    fns = (("plain", lambda: runner.call_varlen(q, k, v, o, None, cuq, cuk, 1, mk_len, False,
-                                                stream=stream.cuda_stream)),
-           ("splitkv", lambda: runner.call_splitkv_varlen(q, k, v, o, None, cuq, cuk, 1, mk_len, False, 0,
-                                                          workspace=ws, stream=stream.cuda_stream)))
-    for name, fn in fns:
-        o.fill_(float("nan"))
-        torch.cuda.synchronize()
-        with torch.cuda.stream(stream):
-            fn()
-        torch.cuda.synchronize()
-        for i in (0, int(np.argmax(klens))):
-            ks, ke = int(cuk_h[i]), int(cuk_h[i + 1])
-            err, _ = check_rows(torch, orc, q[i:i + 1][None], k[ks:ke][None].repeat_interleave(grp, dim=2),
-                                v[ks:ke][None].repeat_interleave(grp, dim=2), o[i:i + 1][None], False,
-                                [(0, 0), (0, vh - 1)])
-            if not orc.check_acceptance_tolerance(err):
-                raise SystemExit(f"api report: varlen decode {name} check failed: {err}")
-        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
-        res[name] = {"us": round(us, 2), "kv_tbps": round(kv_bytes / us / 1e6, 2)}
-        print(f"# varlen decode {name}: {us:.1f} us, K+V {kv_bytes / us / 1e6:.2f} TB/s", file=sys.stderr, flush=True)
-    res["speedup"] = round(res["plain"]["us"] / res["splitkv"]["us"], 2)
-
-    # The same decode batch over paged K/V caches: 64-key pages in a random
-    # order, Auto chunk count; checked like the packed run.
-    ps = 64
-    npg = [-(-int(n) // ps) for n in klens]
-    perm = torch.randperm(sum(npg), generator=torch.Generator().manual_seed(5)).cuda()
-    kc = torch.zeros((sum(npg), ps, vkvh, 128), device="cuda", dtype=torch.bfloat16)
-    vc = torch.zeros_like(kc)
-    table = torch.zeros((vb, max(npg)), device="cuda", dtype=torch.int32)
-    at = 0
-    for i, n in enumerate(npg):
-        ids = perm[at:at + n]
-        at += n
-        table[i, :n] = ids.to(torch.int32)
-        ks, ke = int(cuk_h[i]), int(cuk_h[i + 1])
-        for src, dst in ((k, kc), (v, vc)):
-            pad = torch.zeros((n * ps, vkvh, 128), device="cuda", dtype=torch.bfloat16)
-            pad[:ke - ks] = src[ks:ke]
-            dst[ids] = pad.view(n, ps, vkvh, 128)
-    seqlens = torch.from_numpy(klens.astype(np.int32)).cuda()
-    pws = torch.empty(max(runner.splitkv_paged_workspace_size(vb, vh, vkvh, 1, mk_len, vb, tk, ps, max(npg), sum(npg)),
-                          256), device="cuda", dtype=torch.uint8)
-    fn = lambda: runner.call_splitkv_paged(q, kc, vc, o, None, cuq, seqlens, table, 1, mk_len, 0, workspace=pws,
-                                           total_k=tk, stream=stream.cuda_stream)
-    o.fill_(float("nan"))
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        fn()
-    torch.cuda.synchronize()
-    for i in (0, int(np.argmax(klens))):
-        ks, ke = int(cuk_h[i]), int(cuk_h[i + 1])
-        err, _ = check_rows(torch, orc, q[i:i + 1][None], k[ks:ke][None].repeat_interleave(grp, dim=2),
-                            v[ks:ke][None].repeat_interleave(grp, dim=2), o[i:i + 1][None], False,
-                            [(0, 0), (0, vh - 1)])
-        if not orc.check_acceptance_tolerance(err):
-            raise SystemExit(f"api report: paged decode check failed: {err}")
-    us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
-    res["paged"] = {"page_size": ps, "splits": runner.splitkv_paged_select(vb, vh, vkvh, 1, mk_len, vb, tk, ps,
-                                                                            max(npg), sum(npg)),
-                    "us": round(us, 2), "kv_tbps": round(kv_bytes / us / 1e6, 2)}
-    print(f"# varlen decode paged ({ps}-key pages): {us:.1f} us, K+V {kv_bytes / us / 1e6:.2f} TB/s", file=sys.stderr,
-          flush=True)
-    out["varlen_decode"] = res
-    del q, k, v, o, ws, kc, vc, pws
-    torch.cuda.empty_cache()
     return out
 
 
+# ---------------------------------------------------------------------------
+# Telemetry and provenance
+# ---------------------------------------------------------------------------
 _TELEMETRY = True
 
 
@@ -608,24 +560,6 @@ def _run(cmd, timeout=20, force=False):
         return r.stdout if r.returncode == 0 else None
     except (OSError, subprocess.SubprocessError):
         return None
-
-
-def gpu_clocks():
-    """Current clocks in MHz per domain ({"GFX_0": 2398, ..., "MEM_0": 2000}) from amd-smi, or None."""
-    txt = _run(["amd-smi", "metric", "-c"])
-    if not txt:
-        return None
-    clocks, domain = {}, None
-    for ln in txt.splitlines():
-        t = ln.strip()
-        if t.endswith(":") and " " not in t:
-            domain = t[:-1]
-        elif t.startswith("CLK:") and domain and t.endswith("MHz"):
-            try:
-                clocks[domain] = int(float(t.split()[1]))
-            except ValueError:
-                pass
-    return {d: c for d, c in clocks.items() if d.startswith(("GFX", "MEM"))} or None
 
 
 def gpu_telemetry():
@@ -670,13 +604,6 @@ def gpu_telemetry():
         if sink:
             out[sec] = sink
     return out or None
-
-
-def timed_with_telemetry(fn):
-    """(fn(), amd-smi snapshots before and after it)."""
-    before = gpu_telemetry()
-    res = fn()
-    return res, {"before": before, "after": gpu_telemetry()}
 
 
 def loaded_telemetry(torch, fn, stream, launches=50, max_s=20.0):
@@ -733,7 +660,7 @@ def provenance(torch, lib_path):
             "library_matches_manifest": (lib_entry.get("sha256") == lib_sha) if lib_entry else None,
             "hipcc": next((ln for ln in (hipcc or "").splitlines() if "HIP version" in ln), None),
             "torch": torch.__version__, "device": f"{prop.name} {prop.gcnArchName} {prop.multi_processor_count} CUs",
-            "clocks_before": gpu_clocks()}
+            "host_cpu": cpu_info()}
 
 
 def read_traffic(lib_sha):
@@ -750,50 +677,156 @@ def read_traffic(lib_sha):
     return traffic, counters_sha, (counters_sha != lib_sha)
 
 
-def headline(torch, orc, runner, args, b, h, s, stream, pairs, spin_ms=0.0, observations=None):
-    """Sampled-row check, then graph timing of the dense and causal forward at
-    B{b} H{h} S{s}, each with amd-smi snapshots around its timed region."""
+# ---------------------------------------------------------------------------
+# The driver's line
+# ---------------------------------------------------------------------------
+def _r(x, n):
+    return None if x is None else round(x, n)
+
+
+def make_line(res: dict) -> dict:
+    """The final stdout line from the collected results (pure: no GPU, no I/O).
+
+    `res` keys: b, h, s, config, steps, warmup, dense / causal (us,
+    median_us, tflops, flop, check, check_lse), clk_mhz, traffic,
+    traffic_stale, cpu (cpu_baseline dict or None), comparator (per mask:
+    speedup, sdpa_tflops, max_diff), sweep (name -> us, tflops, frac,
+    roofline_frac, speedup), detail (path), lib_sha256."""
+    b, h, s = res["b"], res["h"], res["s"]
+    dense = res["dense"]
+    clk = res.get("clk_mhz")
+    compulsory = compulsory_bytes(b, h, s, s)
+    frac = dense["tflops"] / PEAK_BF16_TFLOPS
+    roofline = dict(bound="mfma", achieved=_r(dense["tflops"], 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                    frac=round(frac, 4), traffic=res.get("traffic"), traffic_stale=res.get("traffic_stale"),
+                    kernel="fav4::fwd_kernel (dense)", avg_launch_us=_r(dense["us"], 3),
+                    flop_per_launch=dense["flop"], compulsory_hbm_bytes=compulsory,
+                    gfx_mhz_loaded=clk,
+                    frac_at_loaded_clock=_r(dense["tflops"] / (PEAK_BF16_TFLOPS * clk / 2400), 4) if clk else None)
+    cpu = res.get("cpu")
+    cpu_line = None
+    if cpu:
+        cpu_line = dict(value=_r(cpu["value"], 5), unit=cpu["unit"], cores=cpu["cores"], kind=cpu["kind"],
+                        sample=cpu["sample"][:240], fp32_value=(cpu.get("fp32") or {}).get("value"),
+                        cpu_model=(cpu.get("cpu_model") or "")[:80] or None, sockets=cpu.get("sockets"))
+    chk = lambda r: None if r.get("check") is None else [
+        _r(r["check"]["max_abs"], 5), _r((r.get("check_lse") or {}).get("lse_max_abs"), 7)]
+    line = {
+        "metric": METRIC,
+        "value": _r(dense["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": res["steps"],
+        "warmup": res["warmup"],
+        "ms_per_step": _r(dense["us"] / 1000.0, 5),
+        "median_us_per_step": _r(dense["median_us"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) BF16 Q/K/V generated on the GPU)",
+        "config": {"workload": f"FMHA fwd BSHD B{b} H{h} Sq=Sk={s} D128 BF16, scale 1/sqrt(128), LSE off",
+                   "global_batch": b, "seq_len": s, "heads": h, "head_dim": 128, "config_id": res["config"],
+                   "parallelism": "single GPU"},
+        "frac_of_peak_dense": round(frac, 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu_line,
+    }
+    c = res.get("causal")
+    if c:
+        line["causal"] = dict(value=_r(c["tflops"], 2), us=_r(c["us"], 3),
+                              frac=round(c["tflops"] / PEAK_BF16_TFLOPS, 4))
+    line["checks_max_abs_lse"] = {"dense": chk(dense), **({"causal": chk(c)} if c else {})}
+    cmp = res.get("comparator")
+    if cmp:
+        line["comparator"] = {"name": cmp.get("name", "")[:60], **{
+            m: [v["speedup"], v["sdpa_tflops"], v["max_diff"]] for m, v in cmp.items() if isinstance(v, dict)}}
+    sw = res.get("sweep")
+    if sw:
+        line["sweep_cols"] = ["us", "tflops", "frac_of_peak", "frac_of_roofline", "speedup_vs_sdpa"]
+        line["sweep"] = {name: [_r(r["us"], 2), _r(r["tflops"], 1), _r(r["frac"], 4), _r(r["roofline_frac"], 4),
+                                _r(r.get("speedup"), 3)] for name, r in sw.items()}
+    line["library_sha256"] = (res.get("lib_sha256") or "")[:16]
+    line["detail"] = res.get("detail")
+    return line
+
+
+def dump_line(line: dict) -> str:
+    txt = json.dumps(line, separators=(",", ":"))
+    if len(txt.encode()) >= LINE_LIMIT:
+        raise SystemExit(f"bench line is {len(txt.encode())} bytes (limit {LINE_LIMIT})")
+    return txt
+
+
+# ---------------------------------------------------------------------------
+# Special modes
+# ---------------------------------------------------------------------------
+def pmc_pass(torch, runner, args):
+    """Eager launches for rocprofv3 --pmc runs (no graphs, one dispatch per launch)."""
+    b, h, s = args.batch, args.heads, args.seq
     q, k, v = make_inputs(torch, b, h, s)
     o = torch.empty_like(q)
-    out = {}
     for causal in ([False] if args.no_causal else [False, True]):
+        for _ in range(2):
+            runner.call(q, k, v, o, None, causal, args.config)
+        torch.cuda.synchronize()
+        print(f"# pmc-pass launched B{b} H{h} S{s} causal={causal} x2", flush=True)
+    del q, k, v, o
+    src = torch.ones(1 << 28, device="cuda", dtype=torch.float32)    # 1 GiB
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("# pmc-pass copy: 1073741824 bytes read + 1073741824 bytes written per dispatch", flush=True)
+
+
+def mfma_ceiling(torch, runner, pkg, args):
+    """The MFMA rate with nothing else on the chip (libfav4_mfma_ceiling.so,
+    built by build()), at the clock the board's power limit allows, beside
+    the headline kernels measured the same way. One workgroup of 8 waves per
+    CU streams BF16 MFMAs on pseudo-random register operands; shape 0 is
+    32x32x16 (the forward's), shape 1 16x16x32 at equal FLOPs."""
+    import ctypes as C
+    lib = C.CDLL(str(pkg.CEILING_LIB_PATH))
+    lib.fav4_probe_mfma_ceiling.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    lib.fav4_probe_mfma_ceiling.restype = C.c_int
+    stream = torch.cuda.Stream()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 2048                                   # about 2 ms per launch
+    out = torch.empty(cus * 512, device="cuda", dtype=torch.float32)
+    res = {}
+    for shape, name in ((0, "mfma_32x32x16"), (1, "mfma_16x16x32")):
+        fn = lambda: lib.fav4_probe_mfma_ceiling(shape, cus, iters, out.data_ptr(), stream.cuda_stream)
+        with torch.cuda.stream(stream):
+            st = fn()
+        torch.cuda.synchronize()
+        if st:
+            raise SystemExit(f"mfma ceiling probe: HIP status {st}")
+        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+        flop = cus * 8 * iters * 1048576
+        res[name] = dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1),
+                         frac_of_peak=round(flop / us / 1e6 / PEAK_BF16_TFLOPS, 4),
+                         telemetry_under_load=loaded_telemetry(torch, fn, stream) if _TELEMETRY else None)
+        log(f"{name}: {us:.1f} us, {flop / us / 1e6:.1f} TFLOP/s")
+    b, h, s = args.batch, args.heads, args.seq
+    q, k, v = make_inputs(torch, b, h, s)
+    o = torch.empty_like(q)
+    for causal in (False, True):
         fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
-        check = check_lse = None
-        if not args.no_check:
-            o.fill_(float("nan"))
-            torch.cuda.synchronize()   # the fill runs on the default stream
-            with torch.cuda.stream(stream):
-                fn()
-            torch.cuda.synchronize()
-            check, _ = check_rows(torch, orc, q, k, v, o, causal, pairs)
-            if not orc.check_acceptance_tolerance(check):
-                raise SystemExit(f"sampled-row check failed (B{b} H{h} S{s} causal={causal}): {check}")
-            # The same rows with the LSE written (benchmarks/bshd.py:147-156
-            # checks every timed shape with and without it).
-            lse = torch.full((b, h, s), float("nan"), device=q.device, dtype=torch.float32)
-            o.fill_(float("nan"))
-            torch.cuda.synchronize()
-            with torch.cuda.stream(stream):
-                runner.call(q, k, v, o, lse, causal, args.config, stream=stream.cuda_stream)
-            torch.cuda.synchronize()
-            check_lse, _ = check_rows(torch, orc, q, k, v, o, causal, pairs, lse=lse)
-            del lse
-            if not orc.check_acceptance_tolerance(check_lse):
-                raise SystemExit(f"sampled-row LSE check failed (B{b} H{h} S{s} causal={causal}): {check_lse}")
-        samples, tel = timed_with_telemetry(
-            lambda: time_graph(torch, fn, args.steps, args.warmup, observations or args.observations, stream,
-                               spin_ms=spin_ms))
-        flop = flops(b, h, s, s, causal)
-        us = statistics.mean(samples)
-        out[causal] = dict(us=us, median_us=statistics.median(samples), samples_us=samples,
-                           tflops=flop / us / 1e6, flop=flop, check=check, check_lse=check_lse, telemetry=tel)
-        print(f"# B{b} H{h} S{s} causal={causal}: {us:.1f} us/launch, {flop / us / 1e6:.1f} TFLOP/s "
-              f"({flop / us / 1e6 / PEAK_BF16_TFLOPS * 100:.1f}% of peak) check={check} "
-              f"lse_max_abs={None if check_lse is None else check_lse['lse_max_abs']}",
-              file=sys.stderr, flush=True)
-    return out, (q, k, v, o)
+        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+        tflops = flops(b, h, s, s, causal) / us / 1e6
+        res["fwd_causal" if causal else "fwd_dense"] = dict(
+            us=round(us, 2), tflops=round(tflops, 1), frac_of_peak=round(tflops / PEAK_BF16_TFLOPS, 4),
+            telemetry_under_load=loaded_telemetry(torch, fn, stream) if _TELEMETRY else None)
+        log(f"B{b} H{h} S{s} causal={causal}: {us:.1f} us, {tflops:.1f} TFLOP/s")
+    res["fwd_dense_of_ceiling"] = round(res["fwd_dense"]["tflops"] / res["mfma_32x32x16"]["tflops"], 4)
+    print(json.dumps({"mode": "mfma_ceiling", "workload": f"B{b} H{h} Sq=Sk={s} D128 BF16, LSE off, config "
+                      f"{args.config}", "cus": cus, "iters_per_wave": iters, **res}), flush=True)
 
 
+# ---------------------------------------------------------------------------
+# Main
+# ---------------------------------------------------------------------------
 def main():
     args = parse_args()
     global _TELEMETRY
@@ -818,93 +851,123 @@ def main():
     prov = provenance(torch, pkg.LIB_PATH)
     stream = torch.cuda.Stream()
     pairs = [(0, 0), (b // 2, h // 2), (b - 1, h - 1)]
-    results, (q, k, v, o) = headline(torch, orc, runner, args, b, h, s, stream, pairs)
-    dense = results[False]
-    # Clocks, power and temperatures while each headline kernel runs (the
-    # snapshots around the timed regions land when the GPU is already idle).
-    under_load = {}
-    if _TELEMETRY:
-        for causal in results:
-            under_load["causal" if causal else "dense"] = loaded_telemetry(
-                torch, lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream), stream)
-    clk = ((under_load.get("dense") or {}).get("gfx_mhz") or {}).get("mean")
-    # The CPU baseline times the oracle on slices of the same dense inputs.
-    cpu = None if args.no_cpu_baseline else cpu_baseline(torch, orc, q, k, v, args.cpu_seconds)
+    masks = [False] if args.no_causal else [False, True]
+    name = lambda n, causal: f"S{n}_{'causal' if causal else 'dense'}"
+    detail = {"args": vars(args), "provenance": prov, "headline": {}, "sweep": {}}
+    res = dict(b=b, h=h, s=s, config=args.config, steps=args.steps, warmup=args.warmup, lib_sha256=
+               prov["library_sha256"], detail=os.path.relpath(args.detail, ROOT))
 
-    cmp = None
-    if not args.no_comparator:
-        cmp = comparator(torch, orc, runner, q, k, v, o, stream, args, list(results))
+    # Headline: checks, then dedicated graph timing (6 observations).
+    q, k, v = make_inputs(torch, b, h, s)
+    o = torch.empty_like(q)
+    for causal in masks:
+        e = e_lse = None
+        if not args.no_check:
+            e, e_lse = checked(torch, orc, runner, q, k, v, o, causal, args.config, stream, pairs, f"B{b} H{h} S{s}")
+        fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
+        samples = time_graph(torch, fn, args.steps, args.warmup, args.observations, stream)
+        flop = flops(b, h, s, s, causal)
+        us = statistics.mean(samples)
+        r = dict(us=us, median_us=statistics.median(samples), tflops=flop / us / 1e6, flop=flop, check=e,
+                 check_lse=e_lse, samples_us=samples)
+        res["causal" if causal else "dense"] = r
+        detail["headline"][name(s, causal)] = r
+        log(f"B{b} H{h} S{s} causal={causal}: {us:.1f} us/launch, {r['tflops']:.1f} TFLOP/s "
+            f"({r['tflops'] / PEAK_BF16_TFLOPS * 100:.1f}% of peak) check={e}")
+
+    # Clocks, power and temperatures while each headline kernel runs.
+    if _TELEMETRY:
+        under = {}
+        for causal in masks:
+            under[name(s, causal)] = loaded_telemetry(
+                torch, lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream), stream)
+        detail["telemetry_under_load"] = under
+        res["clk_mhz"] = ((under.get(name(s, False)) or {}).get("gfx_mhz") or {}).get("mean")
+
+    res["cpu"] = None if args.no_cpu_baseline else cpu_baseline(torch, orc, q, k, v, args.cpu_seconds)
+    detail["cpu_baseline"] = res["cpu"]
+    if res["cpu"]:
+        log(f"cpu baseline: {res['cpu']['value']:.5f} TFLOP/s FP64 on {res['cpu']['cores']} threads")
+
+    backend = None if args.no_comparator else sdpa_backend(torch)
+    sweep = {}
+    if backend:
+        res["comparator"] = {"name": f"torch SDPA {backend[0]} (torch {torch.__version__})"}
+        sdpa = Sdpa(torch, backend, q, k, v)
+        for causal in masks:
+            a, bs, diff = compare(torch, orc, runner, sdpa, q, k, v, o, causal, args.config, stream, args.steps,
+                                  args.warmup, 0.0)
+            flop = flops(b, h, s, s, causal)
+            cm = dict(speedup=round(statistics.mean(bs) / statistics.mean(a), 3),
+                      sdpa_tflops=round(flop / statistics.mean(bs) / 1e6, 1), max_diff=round(diff, 5))
+            res["comparator"]["causal" if causal else "dense"] = cm
+            detail["headline"][name(s, causal)]["comparator"] = dict(cm, ours_us=a, sdpa_us=bs, order=ABBA)
+            log(f"comparator S{s} causal={causal}: SDPA {cm['sdpa_tflops']} TFLOP/s, ours (interleaved) "
+                f"{flop / statistics.mean(a) / 1e6:.1f}, speedup {cm['speedup']}, max|diff| {diff:.4f}")
+        del sdpa
+    for causal in masks:
+        r = res["causal" if causal else "dense"]
+        sweep[name(s, causal)] = dict(us=r["us"], tflops=r["tflops"], frac=r["tflops"] / PEAK_BF16_TFLOPS,
+                                      roofline_frac=roofline_floor_us(b, h, s, s, causal) / r["us"],
+                                      speedup=(res.get("comparator") or {}).get(
+                                          "causal" if causal else "dense", {}).get("speedup"))
     del q, k, v, o
     torch.cuda.empty_cache()
-    skv = None if args.no_splitkv else splitkv_report(torch, orc, runner, args, stream)
-    api = None if args.no_api else api_report(torch, orc, runner, args, stream)
 
-    # Long-sequence sweep (B and H of the headline): each shape checked on
-    # sampled rows, then graph-timed (2 observations) after an untimed spin-up.
-    sweep = {}
+    # Long-sequence sweep: each shape checked on sampled rows, then timed
+    # against SDPA (interleaved graphs) or alone when no comparator runs.
     for n in ([] if args.no_sweep else [int(x) for x in args.sweep.split(",") if x]):
-        res, bufs = headline(torch, orc, runner, args, b, h, n, stream, pairs, spin_ms=SWEEP_SPIN_MS,
-                             observations=2)
-        del bufs
+        if n == s:
+            continue
+        steps, warmup = sweep_launches(n, args.steps, args.warmup)
+        q, k, v = make_inputs(torch, b, h, n)
+        o = torch.empty_like(q)
+        sdpa = Sdpa(torch, backend, q, k, v) if backend else None
+        for causal in masks:
+            e = e_lse = None
+            if not args.no_check:
+                e, e_lse = checked(torch, orc, runner, q, k, v, o, causal, args.config, stream, pairs,
+                                   f"B{b} H{h} S{n}")
+            flop = flops(b, h, n, n, causal)
+            rec = dict(steps=steps, warmup=warmup, check=e, check_lse=e_lse)
+            if sdpa:
+                a, bs, diff = compare(torch, orc, runner, sdpa, q, k, v, o, causal, args.config, stream, steps,
+                                      warmup, SWEEP_SPIN_MS)
+                rec.update(ours_us=a, sdpa_us=bs, order=ABBA, max_diff=diff,
+                           speedup=statistics.mean(bs) / statistics.mean(a),
+                           sdpa_tflops=flop / statistics.mean(bs) / 1e6)
+            else:
+                a = time_graph(torch, lambda: runner.call(q, k, v, o, None, causal, args.config,
+                                                          stream=stream.cuda_stream),
+                               steps, warmup, args.observations, stream, spin_ms=SWEEP_SPIN_MS)
+                rec.update(ours_us=a)
+            us = statistics.mean(a)
+            rec.update(us=us, tflops=flop / us / 1e6, frac=flop / us / 1e6 / PEAK_BF16_TFLOPS,
+                       roofline_frac=roofline_floor_us(b, h, n, n, causal) / us)
+            sweep[name(n, causal)] = rec
+            detail["sweep"][name(n, causal)] = rec
+            log(f"B{b} H{h} S{n} causal={causal}: {us:.1f} us, {rec['tflops']:.1f} TFLOP/s "
+                f"({rec['frac'] * 100:.1f}% of peak, {rec['roofline_frac'] * 100:.1f}% of roofline)"
+                + (f", SDPA x{rec['speedup']:.3f}, max|diff| {rec['max_diff']:.4f}" if sdpa else "")
+                + f", check max-abs {None if e is None else round(e['max_abs'], 5)}")
+        del q, k, v, o, sdpa
         torch.cuda.empty_cache()
-        for causal, r in res.items():
-            sweep[f"S{n}_{'causal' if causal else 'dense'}"] = dict(
-                us=round(r["us"], 2), tflops=round(r["tflops"], 1),
-                frac_of_peak=round(r["tflops"] / PEAK_BF16_TFLOPS, 4), check=r["check"],
-                check_lse=r["check_lse"], telemetry=r["telemetry"])
+    res["sweep"] = dict(sorted(sweep.items(), key=lambda kv: (int(kv[0][1:].split("_")[0]), kv[0])))
+
+    if args.splitkv:
+        detail["splitkv"] = splitkv_report(torch, orc, runner, args, stream)
+    if args.api:
+        detail["api"] = api_report(torch, orc, runner, args, stream)
 
     traffic, counters_sha, stale = read_traffic(prov["library_sha256"])
-    compulsory = 2 * b * h * 128 * (2 * s + 2 * s)
-    roofline = dict(bound="mfma", achieved=round(dense["tflops"], 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
-                    frac=round(dense["tflops"] / PEAK_BF16_TFLOPS, 4), traffic=traffic,
-                    traffic_library_sha256=counters_sha, traffic_stale=stale,
-                    kernel="fav4::fwd_kernel (dense)", flop_per_launch=dense["flop"],
-                    avg_launch_us=round(dense["us"], 3), compulsory_hbm_bytes=compulsory,
-                    hbm_roofline_tflops=round(dense["flop"] / compulsory * HBM_TBPS, 1),
-                    gfx_clock_mhz_under_load=clk, telemetry_under_load=under_load or None,
-                    peak_at_loaded_clock=round(PEAK_BF16_TFLOPS * clk / 2400, 1) if clk else None,
-                    frac_at_loaded_clock=round(dense["tflops"] / (PEAK_BF16_TFLOPS * clk / 2400), 4) if clk else None)
-    line = {
-        "metric": "fwd TFLOP/s + % BF16 MFMA peak, B32 H8 D128 S4096 dense & causal",
-        "value": round(dense["tflops"], 2),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(dense["us"] / 1000.0, 5),
-        "median_us_per_step": round(dense["median_us"], 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) BF16 Q/K/V generated on the GPU)",
-        "config": {"workload": f"FMHA fwd BSHD B{b} H{h} Sq=Sk={s} D128 BF16, scale 1/sqrt(128), LSE off",
-                   "global_batch": b, "seq_len": s, "heads": h, "head_dim": 128,
-                   "config_id": args.config, "parallelism": "single GPU"},
-        "frac_of_peak_dense": round(dense["tflops"] / PEAK_BF16_TFLOPS, 4),
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-    }
-    if True in results:
-        c = results[True]
-        line["causal"] = dict(value=round(c["tflops"], 2), unit="TFLOP/s", us_per_launch=round(c["us"], 3),
-                              median_us_per_launch=round(c["median_us"], 3),
-                              frac_of_peak=round(c["tflops"] / PEAK_BF16_TFLOPS, 4),
-                              samples_us=[round(x, 2) for x in c["samples_us"]], check=c["check"],
-                              check_lse=c["check_lse"], telemetry=c["telemetry"])
-    line["dense_samples_us"] = [round(x, 2) for x in dense["samples_us"]]
-    line["dense_check"] = dense["check"]
-    line["dense_check_lse"] = dense["check_lse"]
-    line["dense_telemetry"] = dense["telemetry"]
-    line["comparator"] = cmp
-    line["splitkv"] = skv
-    line["api"] = api
-    prov["clocks_after"] = gpu_clocks()
-    prov["host_cpu"] = cpu_info()
-    line["provenance"] = prov
-    if sweep:
-        line["sweep"] = sweep
-    print(json.dumps(line), flush=True)
+    res.update(traffic=traffic, traffic_stale=stale)
+    detail["traffic"] = dict(bytes_per_launch=traffic, counters_library_sha256=counters_sha, stale=stale)
+    line = make_line(res)
+    detail["line"] = line
+    Path(args.detail).parent.mkdir(parents=True, exist_ok=True)
+    Path(args.detail).write_text(json.dumps(detail, indent=1, default=str))
+    log(f"full record written to {args.detail}")
+    print(dump_line(line), flush=True)
 
 
 if __name__ == "__main__":
