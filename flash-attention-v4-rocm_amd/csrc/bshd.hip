@@ -137,7 +137,12 @@ int device_cus() {
 //  * split: rounds * (F + c per 64-key tile of a chunk) + 5 for the merge,
 //    F = 19 and c = 1.8 dense, F = 18 and c = 1.5 causal;
 // where rounds = work items / resident workgroups, rounded up.
-int prefill_auto_splits(const Fav4Args& a, int causal, int max_splits, int ktiles, bool br) {
+// Bottom-right causal (br): the packed (varlen) entry point runs one chunk
+// on its unsplit kernel, one item per (sequence, head, q tile) and no pairs
+// (br_unsplit; priced as rounds * 9 plus the larger of the average work per
+// workgroup slot and the heaviest item); the paged entry point runs one chunk
+// on the split kernels (priced as split_time(1)).
+int prefill_auto_splits(const Fav4Args& a, int causal, int max_splits, int ktiles, bool br, bool br_unsplit) {
     const int64_t cus = device_cus();
     const int64_t bh = int64_t(a.batch) * a.heads;
     const int keys = causal ? std::min(a.sk, a.sq) : a.sk;
@@ -170,9 +175,25 @@ int prefill_auto_splits(const Fav4Args& a, int causal, int max_splits, int ktile
         for (int i = 0; i < nt256; ++i) items += (vis_tiles(256LL * (i + 1)) + tps - 1) / tps;
         return double((bh * items + cus - 1) / cus) * (fixed + per_tile * tps) + 5.0;
     };
-    // Bottom-right causal has no unsplit kernel: one chunk runs the split
-    // kernels too, so it competes under the split model.
-    if (br) best = split_time(1);
+    if (br && br_unsplit) {
+        // fwd_kernel_varlen's tile rule: 128-row tiles for sq <= 1024 or when
+        // 256-row tiles would leave CUs idle (two workgroups per CU), else 256.
+        const bool small = a.sq <= 1024 || bh * ((a.sq + 255) / 256) < cus;
+        const int bm = small ? 128 : 256;
+        const int nt = (a.sq + bm - 1) / bm;
+        const int64_t slots = small ? 2 * cus : cus;
+        int64_t sum = 0;
+        int heavy = 0;
+        for (int i = 0; i < nt; ++i) {
+            const int w = vis_tiles(int64_t(bm) * (i + 1));
+            sum += w;
+            heavy = std::max(heavy, w);
+        }
+        const int64_t rounds = (bh * nt + slots - 1) / slots;
+        best = double(rounds) * 9.0 + std::max(double(bh * sum) / double(slots), double(heavy));
+    } else if (br) {
+        best = split_time(1);
+    }
     int pick = 1;
     for (int s = 2; s <= max_splits; ++s) {
         const double t = split_time(s);
@@ -188,7 +209,7 @@ int prefill_auto_splits(const Fav4Args& a, int causal, int max_splits, int ktile
 // count is then rounded so that no chunk starts past that range.
 // The decode shape packs the query heads that share a K/V head into one row
 // space of (heads / kv_heads) * sq rows per (batch, K/V head).
-SplitPlan split_plan(const Fav4Args& a, int kv_heads, int causal, int req, bool br = false) {
+SplitPlan split_plan(const Fav4Args& a, int kv_heads, int causal, int req, bool br = false, bool br_unsplit = false) {
     const SplitShape sh = split_shape(a);
     const bool pack = sh.bm == 32;
     const int rows = pack ? (a.heads / kv_heads) * a.sq : a.sq;
@@ -206,7 +227,7 @@ SplitPlan split_plan(const Fav4Args& a, int kv_heads, int causal, int req, bool 
         const int auto_max = pack && units <= 2 ? fav4::MAX_SPLITS : sh.auto_max;
         splits = (int64_t(device_cus()) * sh.wgs_per_cu + units - 1) / units;
         splits = std::min<int64_t>(splits, std::min(auto_max, std::max(1, ktiles / MIN_TILES_PER_SPLIT)));
-        if (!pack && splits > 1) splits = prefill_auto_splits(a, causal, int(splits), ktiles, br);
+        if (!pack && splits > 1) splits = prefill_auto_splits(a, causal, int(splits), ktiles, br, br_unsplit);
     }
     splits = std::max<int64_t>(1, std::min<int64_t>(splits, ktiles));
     const int tps = int((ktiles + splits - 1) / splits);
@@ -392,7 +413,7 @@ SplitPlan packed_split_plan(const Fav4Args& a, int kv_heads, int64_t total_k, in
 SplitPlan varlen_split_plan(const Fav4VarlenArgs& v, int causal, int req) {
     const Fav4Args a = varlen_shape(v);
     // Bottom-right prefill: the contiguous prefill plan at the max lengths.
-    if (causal == BOTTOM_RIGHT && a.sq > DECODE_SQ) return split_plan(a, v.kv_heads, 0, req, true);
+    if (causal == BOTTOM_RIGHT && a.sq > DECODE_SQ) return split_plan(a, v.kv_heads, 0, req, true, true);
     return packed_split_plan(a, v.kv_heads, v.total_k, causal == BOTTOM_RIGHT ? 0 : causal, req);
 }
 

@@ -419,16 +419,19 @@ class Runner:
                          total_k, num_pages, page_size, max_pages, 1 / math.sqrt(D))
 
     def splitkv_paged_select(self, batch, heads, kv_heads, max_q, max_k, total_q, total_k, page_size, max_pages,
-                             num_pages) -> int:
+                             num_pages, causal=0) -> int:
+        """Auto chunk count for call_splitkv_paged with the same mask (0 dense, 2 bottom-right)."""
         a = self.paged_shape_args(batch, heads, kv_heads, max_q, max_k, total_q, total_k, page_size, max_pages,
                                   num_pages)
-        return self.hip.fav4_bshd_splitkv_paged_select(C.byref(a), 0)
+        return self.hip.fav4_bshd_splitkv_paged_select(C.byref(a), int(causal))
 
     def splitkv_paged_workspace_size(self, batch, heads, kv_heads, max_q, max_k, total_q, total_k, page_size,
-                                     max_pages, num_pages, splits=0) -> int:
+                                     max_pages, num_pages, splits=0, causal=0) -> int:
+        """Workspace bytes of call_splitkv_paged with the same mask (0 dense, 2 bottom-right):
+        the chunk plan, and so the size, depends on it."""
         a = self.paged_shape_args(batch, heads, kv_heads, max_q, max_k, total_q, total_k, page_size, max_pages,
                                   num_pages)
-        return self.hip.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), 0, int(splits))
+        return self.hip.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), int(causal), int(splits))
 
     def call_splitkv_paged(self, q, k_cache, v_cache, o, lse, cu_q, seqlens_k, block_table, max_q, max_k,
                            splits=0, workspace=None, total_k=None, scale=None, stream=None, causal=0):

@@ -108,7 +108,12 @@ extern "C" int fav4_bshd_splitkv_gqa_select(const Fav4Args* args, int kv_heads, 
 // calls that overlap on one GPU (other streams, other host threads) race and
 // give undefined results; calls ordered on one stream are safe.  The first
 // call on a device looks the array's address up (hipGetSymbolAddress) and
-// returns that lookup's error if it fails.  Allocates nothing.
+// returns that lookup's error if it fails; the address is kept for the life
+// of the process, so after hipDeviceReset of a GPU (which frees the array)
+// this entry point must not be called on that GPU again.  The array belongs
+// to the library's code object: any process that runs this library's
+// kernels on a GPU holds its 64 MiB there, whichever entry points it calls.
+// Allocates nothing.
 extern "C" int fav4_bshd_forward_splitkv_gqa_noalloc(const Fav4Args* args, int kv_heads, int causal, int splits,
                                                      hipStream_t stream);
 

@@ -216,7 +216,7 @@ def _split_plan(b, h, sq, sk, splits, cus=None, causal=False, kvh=None):
     return -(-ktiles // tps), tps
 
 
-def _prefill_auto(b, h, sq, sk, causal, max_splits, ktiles, cus):
+def _prefill_auto(b, h, sq, sk, causal, max_splits, ktiles, cus, br=False, br_unsplit=False):
     """Prefill Auto: the count in 1..max_splits with the lowest predicted time --
     unsplit: rounds of 128-row q tiles (causal: tile pairs), 2 per CU, x (9 +
     c per 64-key tile of a q tile, c = 0.9 with <= 1 workgroup per CU else 1.0;
@@ -225,8 +225,19 @@ def _prefill_auto(b, h, sq, sk, causal, max_splits, ktiles, cus):
     1.5) + 5."""
     keys = min(sk, sq) if causal else sk
     vis = lambda end: -(-min(keys, end if causal else keys) // 64)
+    if br:      # bottom-right: the rows ending at `end` see keys up to end - 1 + sk - sq
+        vis = lambda end: -(-min(keys, max(0, min(end, sq) + sk - sq)) // 64)
     nt128 = -(-sq // 128)
-    if causal:
+    if br and br_unsplit:
+        # packed (varlen) bottom-right, one chunk: the unsplit packed kernel,
+        # one item per (sequence, head, q tile), no pairs
+        small = sq <= 1024 or b * h * -(-sq // 256) < cus
+        bm = 128 if small else 256
+        nt = -(-sq // bm)
+        slots = 2 * cus if small else cus
+        work = [vis(bm * (i + 1)) for i in range(nt)]
+        best = -(-(b * h * nt) // slots) * 9.0 + max(b * h * sum(work) / slots, max(work))
+    elif causal:
         npairs = (nt128 + 1) // 2
         heavy = max(vis(128 * (i + 1)) + (vis(128 * (nt128 - i)) if nt128 - 1 - i != i else 0)
                     for i in range(npairs))
@@ -234,7 +245,11 @@ def _prefill_auto(b, h, sq, sk, causal, max_splits, ktiles, cus):
     else:
         items = b * h * nt128
         best = -(-items // (2 * cus)) * (9.0 + (0.9 if items <= cus else 1.0) * ktiles)
-    fixed, per_tile = (18.0, 1.5) if causal else (19.0, 1.8)
+    fixed, per_tile = (18.0, 1.5) if causal or br else (19.0, 1.8)
+    if br and not br_unsplit:   # paged bottom-right: one chunk runs the split kernels too
+        tps = ktiles
+        items = sum(-(-vis(256 * (i + 1)) // tps) for i in range(-(-sq // 256)))
+        best = -(-(b * h * items) // cus) * (fixed + per_tile * tps) + 5.0
     pick = 1
     for s in range(2, max_splits + 1):
         tps = -(-ktiles // s)
@@ -735,3 +750,46 @@ def test_mfma_ceiling_probe_library():
                                     (0, 65537, 16, 0x1000), (0, 256, 0, 0x1000), (1, 256, (1 << 20) + 1, 0x1000),
                                     (0, 256, 16, None), (1, 256, 16, 0x1002)]:
         assert probe.fav4_probe_mfma_ceiling(shape, grid, iters, out, None) == 1, (shape, grid, iters, out)
+
+
+def test_paged_helpers_forward_the_mask(lib):
+    """Runner.splitkv_paged_select / _workspace_size size the plan of the mask
+    the caller will run: bottom-right prefill of B1 H8 KVH8 Sq=Sk=4096 plans
+    more chunks than dense, so a workspace sized for the dense mask would be
+    too small for a causal=2 call."""
+    pkg = load_package()
+    runner = pkg.Runner()
+    args = (1, 8, 8, 4096, 4096, 4096, 4096, 64, 64, 64)
+    a = pkg.PagedArgs(None, None, None, None, None, None, None, None, 1, 8, 8, 4096, 4096, 4096, 4096, 64, 64, 64,
+                      1 / math.sqrt(128))
+    for causal in (0, 2):
+        assert runner.splitkv_paged_select(*args, causal=causal) == lib.fav4_bshd_splitkv_paged_select(C.byref(a),
+                                                                                                      causal)
+        assert runner.splitkv_paged_workspace_size(*args, causal=causal) == \
+            lib.fav4_bshd_splitkv_paged_workspace_size(C.byref(a), causal, 0)
+    dense = runner.splitkv_paged_workspace_size(*args, causal=0)
+    br = runner.splitkv_paged_workspace_size(*args, causal=2)
+    assert runner.splitkv_paged_select(*args, causal=2) > runner.splitkv_paged_select(*args, causal=0)
+    assert br > dense > 0
+
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 4096), (1, 8, 2048), (1, 8, 8192), (2, 4, 3000), (1, 16, 1500),
+                                   (4, 8, 700), (1, 1, 16384)])
+def test_bottom_right_prefill_plans(lib, shape):
+    """Bottom-right prefill Auto: the packed (varlen) call prices one chunk as
+    its unsplit kernel, the paged call as one split-kernel chunk; both then
+    keep the cheapest count of the closed-form model (max_seqlen_q = max_seqlen_k)."""
+    b, h, s_ = shape
+    pkg = load_package()
+    runner = pkg.Runner()
+    cus = 256
+    ktiles = -(-s_ // 64)
+    cap = min(-(-cus // (b * h * -(-s_ // 256))), min(64, max(1, ktiles // 4)))
+    want_v = _prefill_auto(b, h, s_, s_, False, cap, ktiles, cus, br=True, br_unsplit=True) if cap > 1 else 1
+    want_p = _prefill_auto(b, h, s_, s_, False, cap, ktiles, cus, br=True) if cap > 1 else 1
+    tps_v, tps_p = -(-ktiles // want_v), -(-ktiles // want_p)
+    assert runner.splitkv_varlen_select(b, h, h, s_, s_, b * s_, b * s_, 2) == -(-ktiles // tps_v)
+    pages = -(-s_ // 64)
+    assert runner.splitkv_paged_select(b, h, h, s_, s_, b * s_, b * s_, 64, pages, b * pages, causal=2) == \
+        -(-ktiles // min(tps_p, 64))

@@ -261,7 +261,7 @@ def test_splitkv_bottom_right_causal(gpu_runner, ps):
         assert torch.isnan(ob2[tq:]).all().item() and torch.isnan(lb2[h * tq:]).all().item()
         ws_v = gpu_runner.splitkv_varlen_workspace_size(len(lens), h, kvh, max_q, max_k, tq, len(k), 2, splits)
         ws_p = gpu_runner.splitkv_paged_workspace_size(len(lens), h, kvh, max_q, max_k, tq, len(k), ps,
-                                                       table.shape[1], len(kc), splits)
+                                                       table.shape[1], len(kc), splits, causal=2)
         if ws_v == ws_p:      # same plan (one explicit chunk over 157 key tiles: the paged cap makes 3)
             assert torch.equal(o.view(torch.int16), o2.view(torch.int16)), splits
             assert torch.equal(lse.view(torch.int32), lse2.view(torch.int32)), splits
@@ -318,7 +318,7 @@ def test_splitkv_paged_prefill(gpu_runner, ps):
             _check_bottom_right(o2, lse2, q, k, v, cu_q, cu_k, lens, group, splits)
             ws_v = gpu_runner.splitkv_varlen_workspace_size(len(lens), h, kvh, max_q, max_k, tq, len(k), 2, splits)
             ws_p = gpu_runner.splitkv_paged_workspace_size(len(lens), h, kvh, max_q, max_k, tq, len(k), ps,
-                                                           table.shape[1], len(kc), splits)
+                                                           table.shape[1], len(kc), splits, causal=2)
             if ws_v == ws_p:
                 assert torch.equal(o.view(torch.int16), o2.view(torch.int16)), splits
                 assert torch.equal(lse.view(torch.int32), lse2.view(torch.int32)), splits
@@ -348,3 +348,31 @@ def test_splitkv_paged_prefill(gpu_runner, ps):
     torch.cuda.synchronize()
     assert torch.equal(o.view(torch.int16), oc.view(-1, h, 128).view(torch.int16))
     assert torch.equal(lse.view(torch.int32), lc.permute(1, 0, 2).reshape(h, b * sq).view(torch.int32))
+
+
+def test_splitkv_paged_presized_workspace_bottom_right(gpu_runner):
+    """A caller that sizes the workspace with the helper for the mask it will
+    use (as for graph capture) and passes exactly that buffer: the bottom-right
+    plan of B1 H8 Sq=Sk=4096 has more chunks than the dense one, so a
+    dense-sized buffer would be rejected.  The call succeeds and matches the
+    call that allocates its own workspace, bitwise."""
+    import torch
+    h, kvh, ps = 8, 8, 64
+    dev = torch.device("cuda:0")
+    lens = [(4096, 4096)]
+    q, k, v, kc, vc, cu_q, cu_k, seqlens_k, table = _build(h, kvh, ps, lens, seed=71)
+    qd, kcd, vcd = (to_device(x, dev) for x in (q, kc, vc))
+    cq, sk_d, tb = (torch.from_numpy(x).to(dev) for x in (cu_q, seqlens_k, table))
+    args = (1, h, kvh, 4096, 4096, len(q), len(k), ps, table.shape[1], len(kc))
+    need_dense = gpu_runner.splitkv_paged_workspace_size(*args, 0, causal=0)
+    need_br = gpu_runner.splitkv_paged_workspace_size(*args, 0, causal=2)
+    print(f"  workspace dense {need_dense} B, bottom-right {need_br} B", flush=True)
+    ws = torch.empty(need_br, device=dev, dtype=torch.uint8)
+    _, _, o, lse = _out(torch, dev, len(q), h, True)
+    gpu_runner.call_splitkv_paged(qd, kcd, vcd, o, lse, cq, sk_d, tb, 4096, 4096, 0, workspace=ws, total_k=len(k),
+                                  causal=2)
+    _, _, o2, lse2 = _out(torch, dev, len(q), h, True)
+    gpu_runner.call_splitkv_paged(qd, kcd, vcd, o2, lse2, cq, sk_d, tb, 4096, 4096, 0, total_k=len(k), causal=2)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), o2.view(torch.int16))
+    assert torch.equal(lse.view(torch.int32), lse2.view(torch.int32))

@@ -61,3 +61,63 @@ def test_noalloc_matches_workspace_call(gpu_runner, label, calls):
             e = orc.errors(got[bb:bb + 1, :, hh:hh + 1], lse_h[bb:bb + 1, hh:hh + 1],
                            ref[bb:bb + 1, :, hh:hh + 1], ref_lse[bb:bb + 1, hh:hh + 1])
             assert orc.check_acceptance_tolerance(e), (label, i, bb, hh, e)
+
+
+_CAPTURE_SCRIPT = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import torch
+import __graft_entry__
+pkg = __graft_entry__.import_package()
+r = pkg.Runner()
+dev = torch.device("cuda:0")
+g = torch.Generator(device=dev)
+g.manual_seed(7)
+mk = lambda *s: torch.randn(s, device=dev, dtype=torch.float32, generator=g).to(torch.bfloat16)
+b, h, kvh, sq, sk, causal, splits = 2, 16, 4, 1, 9000, False, 0
+q, k, v = mk(b, sq, h, 128), mk(b, sk, kvh, 128), mk(b, sk, kvh, 128)
+# eager workspace call first (loads the library's code object), then the
+# process's first no-alloc call inside a capture
+ref_o = torch.full_like(q, float("nan"))
+ref_l = torch.full((b, h, sq), float("nan"), device=dev, dtype=torch.float32)
+r.call_splitkv(q, k, v, ref_o, ref_l, causal, splits)
+torch.cuda.synchronize()
+o = torch.full_like(q, float("nan"))
+lse = torch.full((b, h, sq), float("nan"), device=dev, dtype=torch.float32)
+s = torch.cuda.Stream()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=s):
+    r.call_splitkv_noalloc(q, k, v, o, lse, causal, splits, stream=s.cuda_stream)
+for rep in range(3):
+    o.fill_(float("nan"))
+    lse.fill_(float("nan"))
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    same = torch.equal(o.view(torch.int16), ref_o.view(torch.int16)) and \
+        torch.equal(lse.view(torch.int32), ref_l.view(torch.int32))
+    print(f"replay {rep}: bitwise equal to the workspace call: {same}", flush=True)
+    if not same:
+        sys.exit(3)
+    # eager work between replays, on the same array
+    o2 = torch.empty_like(q)
+    r.call_splitkv_noalloc(q, k, v, o2, None, causal, splits)
+    torch.cuda.synchronize()
+    if not torch.equal(o2.view(torch.int16), ref_o.view(torch.int16)):
+        sys.exit(4)
+print("ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """In a fresh process, the first no-alloc call (the one that looks up the
+    per-device array's address) is made while a stream is being captured; the
+    graph is replayed three times, with eager no-alloc calls in between, and
+    every replay is bitwise the workspace call."""
+    import subprocess
+    import sys
+    from tests.conftest import ROOT
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, str(ROOT)], capture_output=True, text=True,
+                       timeout=180)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.returncode
