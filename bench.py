@@ -695,6 +695,7 @@ def make_line(res: dict) -> dict:
     b, h, s = res["b"], res["h"], res["s"]
     dense = res["dense"]
     clk = res.get("clk_mhz")
+    watts = res.get("socket_w")
     compulsory = compulsory_bytes(b, h, s, s)
     frac = dense["tflops"] / PEAK_BF16_TFLOPS
     roofline = dict(bound="mfma", achieved=_r(dense["tflops"], 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
@@ -702,7 +703,9 @@ def make_line(res: dict) -> dict:
                     kernel="fav4::fwd_kernel (dense)", avg_launch_us=_r(dense["us"], 3),
                     flop_per_launch=dense["flop"], compulsory_hbm_bytes=compulsory,
                     gfx_mhz_loaded=clk,
-                    frac_at_loaded_clock=_r(dense["tflops"] / (PEAK_BF16_TFLOPS * clk / 2400), 4) if clk else None)
+                    frac_at_loaded_clock=_r(dense["tflops"] / (PEAK_BF16_TFLOPS * clk / 2400), 4) if clk else None,
+                    socket_w_loaded=watts,
+                    energy_j_per_launch=_r(watts * dense["us"] * 1e-6, 4) if watts else None)
     cpu = res.get("cpu")
     cpu_line = None
     if cpu:
@@ -882,7 +885,9 @@ def main():
             under[name(s, causal)] = loaded_telemetry(
                 torch, lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream), stream)
         detail["telemetry_under_load"] = under
-        res["clk_mhz"] = ((under.get(name(s, False)) or {}).get("gfx_mhz") or {}).get("mean")
+        loaded = under.get(name(s, False)) or {}
+        res["clk_mhz"] = (loaded.get("gfx_mhz") or {}).get("mean")
+        res["socket_w"] = next((v for k, v in (loaded.get("power") or {}).items() if "socket" in k), None)
 
     res["cpu"] = None if args.no_cpu_baseline else cpu_baseline(torch, orc, q, k, v, args.cpu_seconds)
     detail["cpu_baseline"] = res["cpu"]

@@ -37,7 +37,7 @@ def _results():
                 detail="gpurun_out/bench_detail.json",
                 dense=_shape(1885.7, bench.flops(b, h, s, s, False), False),
                 causal=_shape(1068.1, bench.flops(b, h, s, s, True), True),
-                clk_mhz=1843, traffic=1502123456, traffic_stale=False, cpu=cpu,
+                clk_mhz=1843, socket_w=1387, traffic=1502123456, traffic_stale=False, cpu=cpu,
                 comparator={"name": "torch SDPA flash (torch 2.10.0+rocm7.0) " + "z" * 100,
                             "dense": dict(speedup=1.72, sdpa_tflops=678.1, max_diff=0.00098),
                             "causal": dict(speedup=2.61, sdpa_tflops=395.2, max_diff=0.0156)},
@@ -57,8 +57,10 @@ def test_line_fits_and_round_trips():
     assert abs(back["ms_per_step"] - 1.8857) < 1e-9
     r = back["roofline"]
     for key in ("bound", "achieved", "peak", "unit", "frac", "traffic", "traffic_stale", "avg_launch_us",
-                "flop_per_launch", "compulsory_hbm_bytes", "gfx_mhz_loaded", "frac_at_loaded_clock"):
+                "flop_per_launch", "compulsory_hbm_bytes", "gfx_mhz_loaded", "frac_at_loaded_clock",
+                "socket_w_loaded", "energy_j_per_launch"):
         assert key in r, key
+    assert abs(r["energy_j_per_launch"] - 1387 * 1885.7e-6) < 1e-4
     assert r["frac"] == round(r["achieved"] / r["peak"], 4)
     assert r["compulsory_hbm_bytes"] == 2 * 32 * 8 * 128 * 4 * 4096
     c = back["cpu_baseline"]
@@ -72,11 +74,12 @@ def test_line_fits_and_round_trips():
 
 def test_line_without_optional_legs():
     res = _results()
-    for key in ("causal", "cpu", "comparator", "sweep", "clk_mhz"):
+    for key in ("causal", "cpu", "comparator", "sweep", "clk_mhz", "socket_w"):
         res.pop(key)
     back = json.loads(bench.dump_line(bench.make_line(res)))
     assert back["cpu_baseline"] is None
     assert back["roofline"]["frac_at_loaded_clock"] is None
+    assert back["roofline"]["energy_j_per_launch"] is None
     assert "causal" not in back and "sweep" not in back
 
 
