@@ -552,14 +552,28 @@ _TELEMETRY = True
 
 
 def _run(cmd, timeout=20, force=False):
+    """stdout of cmd, or None.  The child runs in its own session; on a
+    time-out its whole process group (helpers it started included) is
+    killed and reaped, so nothing it started outlives the benchmark."""
+    import signal
     import subprocess
     if not (_TELEMETRY or force):
         return None
     try:
-        r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
-        return r.stdout if r.returncode == 0 else None
-    except (OSError, subprocess.SubprocessError):
+        proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                                start_new_session=True)
+    except OSError:
         return None
+    try:
+        out, _ = proc.communicate(timeout=timeout)
+    except subprocess.TimeoutExpired:
+        try:
+            os.killpg(proc.pid, signal.SIGKILL)
+        except OSError:
+            pass
+        proc.communicate()
+        return None
+    return out if proc.returncode == 0 else None
 
 
 def gpu_telemetry():

@@ -96,3 +96,32 @@ def test_sweep_launch_counts():
     assert bench.sweep_launches(16384, 20, 5) == (6, 2)
     assert bench.sweep_launches(32768, 20, 5) == (3, 1)
     assert bench.ABBA.count("A") == bench.ABBA.count("B") == 6
+
+
+def _alive(pid):
+    """True if pid is a live (not zombie) process."""
+    try:
+        with open(f"/proc/{pid}/status") as f:
+            state = [ln for ln in f if ln.startswith("State:")][0]
+    except (OSError, IndexError):
+        return False
+    return "Z" not in state.split()[1]
+
+
+def test_run_helper_output_and_timeout(tmp_path):
+    import time
+    assert bench._run(["echo", "ok"], force=True) == "ok\n"
+    assert bench._run(["false"], force=True) is None
+    assert bench._run(["/nonexistent/tool"], force=True) is None
+    # A command that outlives its time-out, with a helper of its own: both are
+    # killed, and _run returns None.
+    marker = tmp_path / "helper.pid"
+    t0 = time.monotonic()
+    out = bench._run(["bash", "-c", f"sleep 37 & echo $! > {marker}; wait"], timeout=1.0, force=True)
+    assert out is None
+    assert time.monotonic() - t0 < 10
+    pid = int(marker.read_text())
+    deadline = time.monotonic() + 5
+    while _alive(pid) and time.monotonic() < deadline:
+        time.sleep(0.05)
+    assert not _alive(pid)
