@@ -361,6 +361,58 @@ __device__ __forceinline__ void pv_plain(const unsigned char* vs, const LdsOffse
     }
 }
 
+// Epilogue store of one wave's 32 rows, O = acc * inv in BF16.  The MFMA
+// accumulator gives each lane 8-byte pieces of one row, so stores straight
+// from it touch 32 rows (16 bytes each) per instruction, and a workgroup's
+// 64 KiB q tile took 2-3.7 us to leave the CU (measured per wave with
+// s_memrealtime).  Here the wave stages 32 rows x 128 bytes at a time in LDS
+// and each buffer_store_dwordx4 writes 8 rows x 128 contiguous bytes.
+//  * slot: byte offset in smem of 2 KiB of this wave's, plus 2 KiB at
+//    slot + TILE_BYTES, that no other wave reads or writes meanwhile (the
+//    wave's own DMA slots of a stage nobody reads any more).
+//  * 16-byte chunks are XOR-swizzled by row (bank-conflict free writes).
+//  * Rows r >= rows (past the sequence) store nothing: their 32-bit offsets
+//    could wrap into a valid row for large row strides.
+//  * LANE_OPAQUE derives the lane offsets from an opaque copy of the lane
+//    id, so that the compiler does not hoist them out of the item loop and
+//    keep them live through the key loop (where the LSE kernels' register
+//    budget is tight; hoisted, causal LSE spilled).
+template <int TILE_BYTES, bool LANE_OPAQUE>
+__device__ __forceinline__ void store_o_rows(const RowState& st, float inv, unsigned char* smem, uint32_t slot,
+                                             rsrc_t ro, uint32_t orow, int wrow0, int rows, int lane) {
+    static_assert(TILE_BYTES >= 16 * 128, "staging rows");
+    if constexpr (LANE_OPAQUE) asm volatile("" : "+v"(lane));
+    const int col = lane & 31, half = lane >> 5;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int dl = 0; dl < 2; ++dl) {
+#pragma unroll
+            for (int vg = 0; vg < 4; ++vg) {
+                const f32x16& o = st.o[2 * h + dl];
+                const f32x2 x0 = {o[vg * 4 + 0] * inv, o[vg * 4 + 1] * inv};
+                const f32x2 x1 = {o[vg * 4 + 2] * inv, o[vg * 4 + 3] * inv};
+                const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
+                const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
+                // Row col, bytes 64 * db + 16 * vg + 8 * half of the row, i.e.
+                // chunk 4 * dl + vg of its 128-byte half h.
+                const int chunk = 4 * dl + vg;
+                const uint32_t off = slot + (col >> 4) * TILE_BYTES + (col & 15) * 128 +
+                                     ((chunk ^ (col & 7)) << 4) + half * 8;
+                *reinterpret_cast<FAV4_LDS bf16x4*>((FAV4_LDS void*)(smem + off)) = bf16x4{y0[0], y0[1], y1[0], y1[1]};
+            }
+        }
+        // Store i: rows 8i .. 8i+7, lane l writing chunk l % 8 of row 8i + l / 8.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 8 * i + (lane >> 3), c = lane & 7;
+            const uint32_t off = slot + (r >> 4) * TILE_BYTES + (r & 15) * 128 + ((c ^ (r & 7)) << 4);
+            const bf16x8 v = *reinterpret_cast<const FAV4_LDS bf16x8*>((FAV4_LDS const void*)(smem + off));
+            if (r < rows) store16(ro, uint32_t(wrow0 + r) * orow + h * 128 + c * 16, __builtin_bit_cast(f32x4, v));
+        }
+    }
+}
+
 // WAVES waves x 32 query rows per workgroup, BN keys per tile, STAGES LDS
 // buffers of K+V.  Tile t lives in stage t % STAGES; its DMA is issued
 // STAGES-1 tiles ahead (right after barrier t-STAGES+1, into the stage that
@@ -586,17 +638,27 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
         // a valid row when the row stride is large (huge head counts, strided
         // views), and they carry another row's result.
         const float inv = 1.f / st.lb;
-        const uint32_t obase = uint32_t(wave * 32 + col) * L.orow + half * 8;
-        if (row < a.sq) {
+        if constexpr (STAGES == 2) {
+            // The clamped last prefetch went to stage ntiles % 2, which no wave
+            // reads any more: once this wave's own part of that DMA has landed,
+            // its slots there hold the O staging.
+            static_assert(STAGES != 2 || DMA >= 2, "a wave's DMA slots hold 2 KiB per matrix");
+            wait_vmem();
+            store_o_rows<TILE_BYTES, LSE>(st, inv, smem, uint32_t((ntiles & 1) * STAGE_BYTES + wave * DMA * 1024), ro,
+                                          L.orow, wave * 32, a.sq - qw, lane);
+        } else {
+            const uint32_t obase = uint32_t(wave * 32 + col) * L.orow + half * 8;
+            if (row < a.sq) {
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
+                for (int db = 0; db < 4; ++db) {
 #pragma unroll
-                for (int vg = 0; vg < 4; ++vg) {
-                    const f32x2 x0 = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv};
-                    const f32x2 x1 = {st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
-                    const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
-                    const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
-                    store8(ro, obase + (db * 32 + vg * 8) * 2, bf16x4{y0[0], y0[1], y1[0], y1[1]});
+                    for (int vg = 0; vg < 4; ++vg) {
+                        const f32x2 x0 = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv};
+                        const f32x2 x1 = {st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
+                        const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
+                        const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
+                        store8(ro, obase + (db * 32 + vg * 8) * 2, bf16x4{y0[0], y0[1], y1[0], y1[1]});
+                    }
                 }
             }
         }
@@ -605,7 +667,7 @@ void fwd_kernel(Fav4Args a, Layout L, int tiles, int total) {
         if constexpr (LSE) {
             if (half == 0 && row < a.sq) a.lse[int64_t(bh) * a.sq + row] = __builtin_fmaf(st.m, LN2, logf(st.l));
         }
-        wait_vmem();       // clamped prefetches have landed before the stages are reused
+        wait_vmem();       // clamped prefetches and O stores have landed before the stages are reused
         __syncthreads();
     };
     for_each_item<CAUSAL>(tiles, total, process);
@@ -929,6 +991,7 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
     constexpr int STAGE_BYTES = 2 * TILE_BYTES;
     constexpr int DMA = BN / 4 / WAVES;
     static_assert(BN % 32 == 0 && BN % (4 * WAVES) == 0, "tile shape");
+    static_assert(DMA >= 2, "a wave's DMA slots hold 2 KiB per matrix (O staging)");
     __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE_BYTES];
 
     const int lane = threadIdx.x & 63;
@@ -1060,20 +1123,13 @@ void fwd_kernel_varlen(Fav4VarlenArgs a, int tiles, int total) {
         // sequence store nothing (their 32-bit offsets can wrap into a valid
         // row when heads * 256 bytes is large).
         const float inv = st.lb > 0.f ? 1.f / st.lb : 0.f;
-        const uint32_t obase = uint32_t(wave * 32 + col) * row_bytes + half * 8;
-        if (row < sq) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-#pragma unroll
-                for (int vg = 0; vg < 4; ++vg) {
-                    const f32x2 x0 = {st.o[db][vg * 4 + 0] * inv, st.o[db][vg * 4 + 1] * inv};
-                    const f32x2 x1 = {st.o[db][vg * 4 + 2] * inv, st.o[db][vg * 4 + 3] * inv};
-                    const bf16x2 y0 = __builtin_convertvector(x0, bf16x2);
-                    const bf16x2 y1 = __builtin_convertvector(x1, bf16x2);
-                    store8(ro, obase + (db * 32 + vg * 8) * 2, bf16x4{y0[0], y0[1], y1[0], y1[1]});
-                }
-            }
-        }
+        // Stage ntiles % 2 receives no DMA in this q tile and its last tile
+        // (ntiles - 2) was read before the last step's barrier (with fewer
+        // tiles it was never used, and the previous q tile's final wait and
+        // barrier retired everything): this wave's slots there hold the O
+        // staging.
+        store_o_rows<TILE_BYTES, LSE>(st, inv, smem, uint32_t((ntiles & 1) * STAGE_BYTES + wave * DMA * 1024), ro,
+                                      row_bytes, wave * 32, sq - qw, lane);
         if constexpr (LSE) {
             if (half == 0 && row < sq) a.lse[int64_t(head) * a.total_q + qs + row] = __builtin_fmaf(st.m, LN2, logf(st.l));
         }
