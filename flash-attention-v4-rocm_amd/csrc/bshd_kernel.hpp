@@ -370,7 +370,11 @@ __device__ __forceinline__ void pv_plain(const unsigned char* vs, const LdsOffse
 //  * slot: byte offset in smem of 2 KiB of this wave's, plus 2 KiB at
 //    slot + TILE_BYTES, that no other wave reads or writes meanwhile (the
 //    wave's own DMA slots of a stage nobody reads any more).
-//  * 16-byte chunks are XOR-swizzled by row (bank-conflict free writes).
+//  * 16-byte chunks are XOR-swizzled by the row's low 3 bits; a read's 8
+//    lanes cover one whole row.  Each 8-byte write lane uses the first or
+//    second half of a 16-byte chunk, so 32 rows share 16 slots of a bank
+//    window: a 2-way conflict, counted as 64 stall cycles per wave and q tile
+//    (SQ_LDS_BANK_CONFLICT), about 0.2% of a launch.
 //  * Rows r >= rows (past the sequence) store nothing: their 32-bit offsets
 //    could wrap into a valid row for large row strides.
 //  * LANE_OPAQUE derives the lane offsets from an opaque copy of the lane
