@@ -500,16 +500,19 @@ int64_t paged_workspace(const Fav4PagedArgs& v, const SplitPlan& p) {
 }
 
 // Auto: 128-row workgroups (config 1; two per CU, so one's prologue and
-// epilogue overlap the other's key loop) for query lengths up to 1024, and
-// wherever 256-row workgroups (config 2) would leave CUs without a work item
-// (items: q tiles; causal: q-tile pairs); else config 2.  Measured on MI355X
-// (graph-timed, config 1 vs 2): up to Sq 896 config 1 is faster or equal at
-// B32 and B4 H8, at Sq 1024 it loses 1.4% dense and gains 4% causal; with
-// fewer config-2 items than CUs it wins by 28-46% (B1 H8 S2048..S4096, causal
-// B1 H8 S8192, B2 H8 S4096); with one item per CU or more config 2 wins by
-// 6-8% (dense B2 H8 S4096, B1 H32 S4096, causal B1 H32 S4096).
+// epilogue overlap the other's key loop) for query lengths up to 768 (dense)
+// or 1024 (causal), and wherever 256-row workgroups (config 2) would leave
+// CUs without a work item (items: q tiles; causal: q-tile pairs); else
+// config 2.  Measured on MI355X (graph-timed, config 1 vs 2, row-contiguous
+// O stores): dense Sq 512 config 1 wins by 5%, Sq 768 they are equal, Sq 1024
+// config 2 wins by 1.7-6.5% (B32 H8, B16 H8, B8 H8, B4 H16); causal config 1
+// wins or ties up to Sq 1024 (by 26% at B8 H8 and B4 H16 Sq 1024, 17% at B32
+// H8 Sq 768).  With fewer config-2 items than CUs config 1 wins by 28-46%
+// (B1 H8 S2048..S4096, causal B1 H8 S8192, B2 H8 S4096); with one item per
+// CU or more config 2 wins by 6-8% (dense B2 H8 S4096, B1 H32 S4096, causal
+// B1 H32 S4096).
 int auto_config(const Fav4Args& a, int causal) {
-    if (a.sq <= 1024) return 1;
+    if (a.sq <= (causal ? 1024 : 768)) return 1;
     const int64_t tiles = (int64_t(a.sq) + 255) / 256;
     const int64_t items = int64_t(a.batch) * a.heads * (causal ? (tiles + 1) / 2 : tiles);
     return items < device_cus() ? 1 : 2;
@@ -570,8 +573,8 @@ extern "C" __attribute__((visibility("default"))) int fav4_bshd_forward_varlen(c
                                                                        hipStream_t stream) {
     const int st = varlen_ok(a, causal);
     if (st != hipSuccess) return st;
-    // The forward's Auto rule on the longest sequence: 128-row tiles (4 waves)
-    // for max_seqlen_q <= 1024 or when 256-row tiles would give fewer
+    // Tile rule on the longest sequence: 128-row tiles (4 waves) for
+    // max_seqlen_q <= 1024 or when 256-row tiles would give fewer
     // (sequence, head, q tile) items than CUs; else 256-row tiles.
     const int64_t tiles256 = (int64_t(a->max_seqlen_q) + 255) / 256;
     const bool small = a->max_seqlen_q <= 1024 || int64_t(a->batch) * a->heads * tiles256 < device_cus();

@@ -29,9 +29,10 @@ struct Fav4Args {
 //
 // Config IDs (gfx950 tile shapes; BM = query rows per workgroup, BN = keys per
 // K/V tile, 32 query rows per wave64):
-//  0: Auto: config 1 for sq <= 1024 or when config 2 would have fewer work
-//     items than the device has CUs (items: B*H*ceil(sq/256) q tiles; causal:
-//     B*H*ceil(ceil(sq/256)/2) q-tile pairs), else config 2
+//  0: Auto: config 1 for sq <= 768 (dense) or sq <= 1024 (causal), or when
+//     config 2 would have fewer work items than the device has CUs (items:
+//     B*H*ceil(sq/256) q tiles; causal: B*H*ceil(ceil(sq/256)/2) q-tile
+//     pairs), else config 2
 //  1: BM 128 / BN 64, 4 waves, 2 LDS stages
 //  2: BM 256 / BN 64, 8 waves, 2 LDS stages
 //  3: BM 256 / BN 64, 8 waves, 3 LDS stages with QK^T(t+1) pipelined

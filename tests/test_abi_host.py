@@ -143,12 +143,13 @@ def test_rejects_null_args(lib):
 
 
 @pytest.mark.parametrize("b,h,sq,want", [
-    (2, 4, 1, 1), (2, 4, 127, 1), (32, 8, 256, 1), (32, 8, 1000, 1), (32, 8, 1024, 1),   # Sq <= 1024: config 1
+    (2, 4, 1, 1), (2, 4, 127, 1), (32, 8, 256, 1), (32, 8, 768, 1),   # Sq <= 768: config 1
+    (32, 8, 769, 2), (32, 8, 1000, 2), (32, 8, 1024, 2), (4, 16, 1024, 2), (2, 4, 1000, 1),
     (32, 8, 1025, 2), (32, 8, 4096, 2), (32, 8, 32768, 2), (2, 8, 4096, 2), (1, 32, 4096, 2),
     (1, 8, 4096, 1), (1, 8, 8192, 2), (2, 4, 4096, 1), (1, 1, 32768, 1)])   # fewer q tiles than 256 CUs: config 1
 def test_select_config(lib, Args, b, h, sq, want):
     """Closed form of Auto for a dense call on 256 CUs (the library's value
-    when no device is visible): config 1 for Sq <= 1024 or fewer than 256
+    when no device is visible): config 1 for Sq <= 768 or fewer than 256
     q tiles of 256 rows, else config 2."""
     fields = _good(Args)
     fields.update(batch=b, heads=h, sq=sq)
@@ -158,20 +159,21 @@ def test_select_config(lib, Args, b, h, sq, want):
 
 
 @pytest.mark.parametrize("b,h,sq,want", [
-    (32, 8, 1024, 1), (32, 8, 4096, 2), (1, 32, 4096, 2), (1, 64, 4096, 2), (2, 16, 4096, 2),
+    (32, 8, 768, 1), (32, 8, 1024, 1), (32, 8, 4096, 2), (1, 32, 4096, 2), (1, 64, 4096, 2), (2, 16, 4096, 2),
     (1, 16, 4096, 1), (1, 8, 8192, 1), (1, 8, 16384, 2), (1, 1, 32768, 1)])
 def test_select_config_masked_causal(lib, Args, b, h, sq, want):
     """Closed form of Auto for a causal call on 256 CUs: config 1 for
     Sq <= 1024 or fewer than 256 q-tile pairs (B*H*ceil(ceil(Sq/256)/2)),
     else config 2.  The masks disagree at B1 H16 S4096 and B1 H8 S8192: 256
-    q tiles (dense: config 2) but 128 pairs (causal: config 1)."""
+    q tiles (dense: config 2) but 128 pairs (causal: config 1); and at
+    B32 H8 S1024, where the dense cut-off (Sq 768) gives config 2."""
     fields = _good(Args)
     fields.update(batch=b, heads=h, sq=sq)
     tiles = (sq + 255) // 256
     pairs = b * h * ((tiles + 1) // 2)
     assert want == (1 if sq <= 1024 or pairs < 256 else 2)
     assert lib.fav4_bshd_select_config_masked(C.byref(Args(**fields)), 1) == want
-    if (b, h, sq) in ((1, 16, 4096), (1, 8, 8192)):
+    if (b, h, sq) in ((1, 16, 4096), (1, 8, 8192), (32, 8, 1024)):
         assert lib.fav4_bshd_select_config(C.byref(Args(**fields))) == 2
 
 
