@@ -18,10 +18,10 @@
 //  * O^T += V^T.P^T: P leaves the S accumulator directly as the B operand
 //    (no LDS round trip); the V operand comes from ds_read_b64_tr_b16.
 //  * Key tiles that no row of the workgroup masks run a branch-free body;
-//    only the causal-diagonal and key-tail tiles run the masked body, where
-//    QK^T skips 32-key blocks entirely hidden from a wave, the rest get the
-//    element mask, and a wave skips a causal tile entirely above its rows.
-//    Key tiles entirely above the diagonal are never loaded.
+//    only the causal-diagonal and key-tail tiles run the masked body, which
+//    computes every 32-key block and then masks scores element by element; a
+//    wave skips a causal tile entirely above its rows.  Key tiles entirely
+//    above the diagonal are never loaded.
 //  * O is normalised by the sum of the BF16-rounded weights that entered the
 //    PV product (see the epilogue); the LSE uses the FP32 sum as the reference.
 #pragma once
