@@ -7,7 +7,11 @@ seeded), scale 1/sqrt(128), LSE off -- timed dense (the JSON ``value``) and
 top-left causal (reported beside it).  Timing follows the reference harness,
 benchmarks/bshd.py:34-51,163: a HIP graph of W launches is replayed as warmup,
 then a graph of exactly K launches is replayed between two GPU events on the
-launch stream; six such observations are taken and the mean is reported.  The
+launch stream; six such observations are taken and the mean is reported.
+Before the first observation of every timed shape the warmup graph replays,
+untimed, for 50 ms: the FP64 checks run on the CPU while the GPU idles, and
+without the spin-up the first observation caught the clock's ramp back to its
+loaded value (3% slow dense, 8% causal, where the other five agree).  The
 FLOP convention is the reference's (bshd.py:169-170, README.md:59): useful
 QK+PV only, dense 4*B*H*D*S^2, causal 4*B*H*D*S(S+1)/2.
 
@@ -52,7 +56,7 @@ METRIC = "fwd TFLOP/s + % BF16 MFMA peak, B32 H8 D128 S4096 dense & causal"
 PEAK_BF16_TFLOPS = 2516.6      # MI355X dense BF16 MFMA: 256 CU x 4 SIMD x 1024 FLOP/clk x 2.4 GHz
 HBM_TBPS = 8.0
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_fmha_fwd_dense_b32h8s4096.md"
-SWEEP_SPIN_MS = 50.0           # untimed spin-up before each sweep shape
+SPIN_MS = 50.0                 # untimed spin-up before each timed shape (headline and sweep)
 DEFAULT_SWEEP = "512,1024,2048,8192,16384,32768"   # bshd.py:195 plus the long-sequence configs
 ABBA = "ABBABAABABBA"          # bshd.py:151-166: six observations of each side
 LINE_LIMIT = 4096              # bytes of the final stdout line
@@ -453,7 +457,7 @@ def splitkv_report(torch, orc, runner, args, stream):
             err, _ = check_rows(torch, orc, q, k, v, o, causal, [(0, 0), (0, h - 1)])
             if not orc.check_acceptance_tolerance(err):
                 raise SystemExit(f"split-KV report: {name} check failed ({label}): {err}")
-            us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+            us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SPIN_MS))
             res[name] = dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1))
         res["speedup"] = round(res["plain"]["us"] / res["splitkv"]["us"], 2)
         out[label] = res
@@ -534,7 +538,7 @@ def api_report(torch, orc, runner, args, stream, b=32, h=8, s=4096, kvh=2):
                             v[i:i + 1].repeat_interleave(grp, dim=2), o[i:i + 1], False, [(0, 0), (0, dh - 1)])
         if not orc.check_acceptance_tolerance(err):
             raise SystemExit(f"api report: gqa decode check failed: {err}")
-    us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+    us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SPIN_MS))
     kv_bytes = 2 * db * dsk * dkvh * 256
     splits = runner.splitkv_select(db, dh, 1, dsk, False, kv_heads=dkvh)
     log(f"gqa decode (split-KV, {splits} chunks): {us:.1f} us, K+V {kv_bytes / us / 1e6:.2f} TB/s")
@@ -819,7 +823,7 @@ def mfma_ceiling(torch, runner, pkg, args):
         torch.cuda.synchronize()
         if st:
             raise SystemExit(f"mfma ceiling probe: HIP status {st}")
-        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SPIN_MS))
         flop = cus * 8 * iters * 1048576
         res[name] = dict(us=round(us, 2), tflops=round(flop / us / 1e6, 1),
                          frac_of_peak=round(flop / us / 1e6 / PEAK_BF16_TFLOPS, 4),
@@ -830,7 +834,7 @@ def mfma_ceiling(torch, runner, pkg, args):
     o = torch.empty_like(q)
     for causal in (False, True):
         fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
-        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SWEEP_SPIN_MS))
+        us = statistics.mean(time_graph(torch, fn, args.steps, args.warmup, 3, stream, spin_ms=SPIN_MS))
         tflops = flops(b, h, s, s, causal) / us / 1e6
         res["fwd_causal" if causal else "fwd_dense"] = dict(
             us=round(us, 2), tflops=round(tflops, 1), frac_of_peak=round(tflops / PEAK_BF16_TFLOPS, 4),
@@ -882,7 +886,7 @@ def main():
         if not args.no_check:
             e, e_lse = checked(torch, orc, runner, q, k, v, o, causal, args.config, stream, pairs, f"B{b} H{h} S{s}")
         fn = lambda: runner.call(q, k, v, o, None, causal, args.config, stream=stream.cuda_stream)
-        samples = time_graph(torch, fn, args.steps, args.warmup, args.observations, stream)
+        samples = time_graph(torch, fn, args.steps, args.warmup, args.observations, stream, spin_ms=SPIN_MS)
         flop = flops(b, h, s, s, causal)
         us = statistics.mean(samples)
         r = dict(us=us, median_us=statistics.median(samples), tflops=flop / us / 1e6, flop=flop, check=e,
@@ -951,14 +955,14 @@ def main():
             rec = dict(steps=steps, warmup=warmup, check=e, check_lse=e_lse)
             if sdpa:
                 a, bs, diff = compare(torch, orc, runner, sdpa, q, k, v, o, causal, args.config, stream, steps,
-                                      warmup, SWEEP_SPIN_MS)
+                                      warmup, SPIN_MS)
                 rec.update(ours_us=a, sdpa_us=bs, order=ABBA, max_diff=diff,
                            speedup=statistics.mean(bs) / statistics.mean(a),
                            sdpa_tflops=flop / statistics.mean(bs) / 1e6)
             else:
                 a = time_graph(torch, lambda: runner.call(q, k, v, o, None, causal, args.config,
                                                           stream=stream.cuda_stream),
-                               steps, warmup, args.observations, stream, spin_ms=SWEEP_SPIN_MS)
+                               steps, warmup, args.observations, stream, spin_ms=SPIN_MS)
                 rec.update(ours_us=a)
             us = statistics.mean(a)
             rec.update(us=us, tflops=flop / us / 1e6, frac=flop / us / 1e6 / PEAK_BF16_TFLOPS,
